@@ -1,0 +1,86 @@
+"""ctypes binding of libflicker_hip.so (the C ABI declared in include/flicker_hip.h).
+
+The library is the only compute path of this package: if it has not been built the
+first call raises ``HipLibraryMissing`` -- there is no CPU or PyTorch fallback.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import pathlib
+
+import torch
+
+LIB_PATH = pathlib.Path(__file__).resolve().with_name("libflicker_hip.so")
+
+_p, _i, _i64, _f = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
+_ip = ctypes.POINTER(ctypes.c_int)
+
+# name -> (restype, argtypes); one entry per function of include/flicker_hip.h
+SIGNATURES = {
+    "flk_abi_version": (_i, []),
+    "flk_status_string": (ctypes.c_char_p, [_i]),
+    "flk_qk_prep": (_i, [_p, _i64, _i64, _p, _p, _i64, _p, _p, _i, _f, _i, _i, _i, _i,
+                         _p, _p, _p, _i64, _i64, _p]),
+    "flk_attend": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _p]),
+    "flk_rope_embed": (_i, [_p, _i64, _i64, _i, _ip, _f, _p, _p]),
+    "flk_lane_pair": (_i, [_p, _i64, _i, _p, _p, _p]),
+    "flk_rope_lanes": (_i, [_p, _i64, _i64, _i, _ip, _f, _p, _p, _p]),
+}
+
+ABI_VERSION = 1
+FLK_OK, FLK_E_INVALID, FLK_E_ALIGN, FLK_E_UNSUPPORTED = 0, -1, -2, -3
+
+
+class HipLibraryMissing(RuntimeError):
+    """libflicker_hip.so is not built (run ``python -m flicker_amd.build``)."""
+
+
+class HipKernelError(RuntimeError):
+    """A C-ABI entry point returned a non-zero status."""
+
+
+_LIB = None
+
+
+def lib() -> ctypes.CDLL:
+    """Load the library once and attach the argument types of every entry point."""
+    global _LIB
+    if _LIB is None:
+        if not LIB_PATH.exists():
+            raise HipLibraryMissing(
+                f"{LIB_PATH} is missing: build it with `python -m flicker_amd.build` "
+                "(flicker_amd has no fallback compute path)")
+        handle = ctypes.CDLL(str(LIB_PATH))
+        for name, (restype, argtypes) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        version = handle.flk_abi_version()
+        if version != ABI_VERSION:
+            raise HipLibraryMissing(f"{LIB_PATH} has ABI {version}, expected {ABI_VERSION}; rebuild it")
+        _LIB = handle
+    return _LIB
+
+
+def status_string(status: int) -> str:
+    return lib().flk_status_string(status).decode()
+
+
+def check(status: int, what: str) -> None:
+    if status != FLK_OK:
+        raise HipKernelError(f"{what} failed with status {status}: {status_string(status)}")
+
+
+def stream_of(t: torch.Tensor) -> int:
+    """Raw hipStream_t of torch's current stream on the tensor's device."""
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def int_array(values) -> ctypes.Array:
+    values = [int(v) for v in values]
+    return (ctypes.c_int * len(values))(*values)

@@ -1,0 +1,202 @@
+"""Drop-in replacements for kelechi-c/flicker's ``kernels`` module (src/flicker/kernels.py).
+
+Same names, call signatures, argument meaning and errors as the reference, over torch
+tensors on an MI355X; every computation runs in the HIP kernels of libflicker_hip.so.
+
+  Freqs, EPS, ROW_TILES, row_tile, lane_pair     kernels.py:12-31
+  qk_prep                                         kernels.py:57-91  -> flk_qk_prep
+  SCORE_TILES, EXP_LIMIT, logit_bound             kernels.py:94-101
+  attend                                          kernels.py:105-145 -> flk_attend
+
+Beyond the reference, ``qk_prep`` takes optional ``out=(q, k, v)`` / ``out_offset`` so
+the text and image streams of a double block can be written straight into one
+concatenated buffer, and it accepts a strided ``qkv`` view (e.g. the qkv part of a
+single block's fused linear1 output) without a copy.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import NamedTuple
+
+import torch
+
+from . import _lib
+
+HEAD_DIM = 128  # the only head width the HIP kernels are built for (Klein 4B: 3072 / 24)
+
+
+class Freqs(NamedTuple):
+    """kernels.py:12-16 -- (L, 128) float32 cos / sin lane tables and the static query gain."""
+
+    cos: torch.Tensor
+    sin: torch.Tensor
+    q_gain: float = 1.0
+
+
+EPS = 1e-6
+ROW_TILES = (2304, 1536, 1152, 512, 256, 128, 64)
+
+
+def row_tile(length: int) -> int | None:
+    """kernels.py:23-24 -- the first row tile dividing ``length``, else None."""
+    for size in ROW_TILES:
+        if length % size == 0:
+            return size
+    return None
+
+
+def _on_gpu(name: str, t: torch.Tensor) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor, got {type(t).__name__}")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} is on {t.device}; flicker_amd runs its kernels on the GPU only")
+
+
+def _dense_rows(t: torch.Tensor) -> torch.Tensor:
+    """Keep a view whose last axis is contiguous and whose other strides keep 16-byte rows;
+    anything else is compacted on the device first."""
+    ok = t.stride(-1) == 1 and all(s % 8 == 0 for s in t.stride()[:-1]) and t.data_ptr() % 16 == 0
+    return t if ok else t.contiguous()
+
+
+def lane_pair(freqs: torch.Tensor, q_gain: float = 1.0) -> Freqs:
+    """kernels.py:28-31 -- rope table (1, 1, L, P, 2, 2) -> (L, 2P) cos / sin lanes
+    (batch 0, head-broadcast 0), computed by flk_lane_pair."""
+    _on_gpu("freqs", freqs)
+    if freqs.dim() < 3 or freqs.shape[-2:] != (2, 2):
+        raise ValueError(f"freqs must end in (..., L, P, 2, 2), got {tuple(freqs.shape)}")
+    pe = freqs
+    while pe.dim() > 4:
+        pe = pe[0]
+    pe = pe.to(torch.float32).contiguous()
+    length, pairs = pe.shape[0], pe.shape[1]
+    cos = torch.empty((length, 2 * pairs), dtype=torch.float32, device=pe.device)
+    sin = torch.empty_like(cos)
+    _lib.check(_lib.lib().flk_lane_pair(pe.data_ptr(), length, pairs, cos.data_ptr(), sin.data_ptr(),
+                                        _lib.stream_of(pe)), "flk_lane_pair")
+    return Freqs(cos, sin, float(q_gain))
+
+
+def _launch_qk_prep(qkv, q_scale, k_scale, freqs: Freqs, num_heads: int, out, out_offset: int):
+    batch, length, width = qkv.shape
+    head_dim = width // (3 * num_heads)
+    if 3 * num_heads * head_dim != width:
+        raise ValueError(f"qkv width {width} is not 3 * num_heads({num_heads}) * head_dim")
+    if head_dim != HEAD_DIM:
+        raise ValueError(f"qk_prep: head_dim {head_dim} unsupported (kernels are built for {HEAD_DIM})")
+    if qkv.dtype != torch.bfloat16:
+        raise TypeError(f"qkv must be bfloat16, got {qkv.dtype}")
+    cos, sin, q_gain = freqs
+    for name, t in (("freqs.cos", cos), ("freqs.sin", sin), ("q_scale", q_scale), ("k_scale", k_scale)):
+        _on_gpu(name, t)
+    if cos.shape != (length, head_dim) or sin.shape != (length, head_dim):
+        raise ValueError(f"freqs tables must be ({length}, {head_dim}), got {tuple(cos.shape)} / {tuple(sin.shape)}")
+    if cos.dtype != torch.float32 or sin.dtype != torch.float32:
+        raise TypeError("freqs.cos / freqs.sin must be float32")
+    if q_scale.numel() != head_dim or k_scale.numel() != head_dim:
+        raise ValueError(f"q_scale / k_scale must hold {head_dim} values")
+    if q_scale.dtype != k_scale.dtype or q_scale.dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError("q_scale and k_scale must share one dtype, bfloat16 or float32")
+    qkv = _dense_rows(qkv)
+    cos = cos if cos.stride(1) == 1 and cos.stride(0) % 4 == 0 and cos.data_ptr() % 16 == 0 else cos.contiguous()
+    sin = sin if sin.stride(1) == 1 and sin.stride(0) % 4 == 0 and sin.data_ptr() % 16 == 0 else sin.contiguous()
+    if sin.stride(0) != cos.stride(0):
+        cos, sin = cos.contiguous(), sin.contiguous()
+    q_scale = q_scale.reshape(-1).contiguous()
+    k_scale = k_scale.reshape(-1).contiguous()
+
+    if out is None:
+        if out_offset:
+            raise ValueError("out_offset needs out=(q, k, v)")
+        shape = (batch, num_heads, length, head_dim)
+        out = tuple(torch.empty(shape, dtype=torch.bfloat16, device=qkv.device) for _ in range(3))
+        out_length = length
+    else:
+        out = tuple(out)
+        if len(out) != 3:
+            raise ValueError("out must be a (q, k, v) triple")
+        out_length = out[0].shape[2]
+        for t in out:
+            _on_gpu("out", t)
+            if (t.dtype != torch.bfloat16 or t.dim() != 4 or t.shape[0] != batch or t.shape[1] != num_heads
+                    or t.shape[3] != head_dim or t.shape[2] != out_length or not t.is_contiguous()):
+                raise ValueError("out tensors must be contiguous bf16 (B, H, L_out, D) of one shape")
+        if out_offset < 0 or out_offset + length > out_length:
+            raise ValueError(f"out_offset {out_offset} + L {length} exceeds the output length {out_length}")
+
+    status = _lib.lib().flk_qk_prep(
+        qkv.data_ptr(), qkv.stride(0), qkv.stride(1), cos.data_ptr(), sin.data_ptr(), cos.stride(0),
+        q_scale.data_ptr(), k_scale.data_ptr(), int(q_scale.dtype == torch.float32), float(q_gain),
+        batch, length, num_heads, head_dim, out[0].data_ptr(), out[1].data_ptr(), out[2].data_ptr(),
+        out_length, out_offset, _lib.stream_of(qkv))
+    _lib.check(status, "flk_qk_prep")
+    return out
+
+
+def qk_prep(qkv: torch.Tensor, q_scale: torch.Tensor, k_scale: torch.Tensor, freqs: Freqs,
+            num_heads: int, *, rows: int | None = None, interpret: bool = False,
+            out=None, out_offset: int = 0):
+    """kernels.py:57-91 -- fused head transpose + QK-RMSNorm + RoPE (+ q_gain on q).
+
+    qkv (B, L, 3*H*D) bf16 -> q, k, v (B, H, L, D) bf16.  As in the reference, ``rows``
+    (or the default row tile) must divide L; the HIP kernel itself tiles by 16 tokens."""
+    if interpret:
+        raise ValueError("interpret=True is Pallas' CPU emulation; flicker_amd has one HIP path")
+    _on_gpu("qkv", qkv)
+    if qkv.dim() != 3:
+        raise ValueError(f"qkv must be (B, L, 3*H*D), got {tuple(qkv.shape)}")
+    length = qkv.shape[1]
+    tile_rows = rows or row_tile(length)
+    if tile_rows is None or length % tile_rows:
+        raise ValueError(f"qk_prep needs a row tile dividing L={length} (rows={tile_rows})")
+    return _launch_qk_prep(qkv, q_scale, k_scale, freqs, num_heads, out, out_offset)
+
+
+SCORE_TILES = (2304, 1536, 1152, 512, 256, 128)
+EXP_LIMIT = 80.0
+
+
+def logit_bound(q_scale, k_scale):
+    """kernels.py:99-101 -- sqrt(D) * max|q_scale| * max|k_scale| over the last axis: an upper
+    bound on |q.k|/sqrt(D) after QK-RMSNorm (unit-RMS rows, orthogonal RoPE, Cauchy-Schwarz)."""
+    q_scale = torch.as_tensor(q_scale, dtype=torch.float32)
+    k_scale = torch.as_tensor(k_scale, dtype=torch.float32)
+    width = q_scale.shape[-1]
+    return math.sqrt(width) * q_scale.abs().amax(-1) * k_scale.abs().amax(-1)
+
+
+def attend(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, block: int | None = None,
+           interpret: bool = False, out: torch.Tensor | None = None) -> torch.Tensor:
+    """kernels.py:105-145 -- bounded flash attention (no running max), q pre-scaled by
+    1/sqrt(D).  q, k, v (B, H, L, D) bf16 -> o (B, H, L, D) bf16."""
+    if interpret:
+        raise ValueError("interpret=True is Pallas' CPU emulation; flicker_amd has one HIP path")
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        _on_gpu(name, t)
+        if t.dtype != torch.bfloat16:
+            raise TypeError(f"{name} must be bfloat16, got {t.dtype}")
+        if t.dim() != 4:
+            raise ValueError(f"{name} must be (B, H, L, D), got {tuple(t.shape)}")
+    if not (q.shape == k.shape == v.shape):
+        raise ValueError(f"q, k, v shapes differ: {tuple(q.shape)} {tuple(k.shape)} {tuple(v.shape)}")
+    batch, heads, length, dim = q.shape
+    block = block or next(size for size in SCORE_TILES if length % size == 0)
+    if length % block:
+        raise ValueError(f"attend block {block} does not divide L={length}")
+    if dim != HEAD_DIM:
+        raise ValueError(f"attend: head_dim {dim} unsupported (kernels are built for {HEAD_DIM})")
+    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    if out is None:
+        out = torch.empty_like(q)
+    elif out.shape != q.shape or out.dtype != torch.bfloat16 or not out.is_contiguous():
+        raise ValueError("out must be a contiguous bf16 tensor shaped like q")
+    _launch_attend(q, k, v, out)
+    return out
+
+
+def _launch_attend(q, k, v, out) -> None:
+    batch, heads, length, dim = q.shape
+    status = _lib.lib().flk_attend(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                                   batch, heads, length, dim, _lib.stream_of(q))
+    _lib.check(status, "flk_attend")

@@ -1,0 +1,69 @@
+"""The attention sections of the Klein DiT blocks, wired to the HIP kernels.
+
+Reference: src/flicker/modules.py -- heads :56-60, merge_heads :63-65, qkv_prep :68-80,
+double_prepare_qkv :96-140 with double_block :156-158, single_prepare_qkv :180-191 with
+single_block :197-198.  These functions take the already-projected QKV activations
+(the linear/modulate parts of the blocks are outside this path) and return the
+merged attention output, in the same order and layout as the reference.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .kernels import Freqs, _launch_qk_prep, attend, lane_pair
+
+
+def heads(qkv: torch.Tensor, num_heads: int):
+    """modules.py:56-60 -- (B, L, 3*H*D) -> three (B, H, L, D) views (no copy)."""
+    b, length, width = qkv.shape
+    head_dim = width // (3 * num_heads)
+    split = qkv.reshape(b, length, 3, num_heads, head_dim).permute(2, 0, 3, 1, 4)
+    return split[0], split[1], split[2]
+
+
+def merge_heads(x: torch.Tensor) -> torch.Tensor:
+    """modules.py:63-65 -- (B, H, L, D) -> (B, L, H*D)."""
+    b, h, n, d = x.shape
+    return x.transpose(1, 2).reshape(b, n, h * d)
+
+
+def qkv_prep(qkv, q_scale, k_scale, pe, freqs: Freqs | None, num_heads: int, *, out=None,
+             out_offset: int = 0):
+    """modules.py:68-80 -- QK-RMSNorm + RoPE + head split.  The reference switches between its
+    fused kernel and a plain-XLA branch; here both are the one HIP kernel: without ``freqs``
+    the lane tables are built from ``pe`` with gain 1 (the plain branch applies no q_gain),
+    and any L is accepted (the plain branch has no row-tile condition)."""
+    if freqs is None:
+        freqs = lane_pair(pe, 1.0)
+    return _launch_qk_prep(qkv, q_scale, k_scale, freqs, num_heads, out, out_offset)
+
+
+def _slice(freqs: Freqs, start: int, stop: int) -> Freqs:
+    return Freqs(freqs.cos[start:stop], freqs.sin[start:stop], freqs.q_gain)
+
+
+def double_attention(txt_qkv, img_qkv, txt_scales, img_scales, freqs: Freqs, num_heads: int):
+    """modules.py:127-139 + 157-158 -- per-stream qk prep, joint text|image attention, merge,
+    split back into (txt_attn, img_attn), each (B, L_stream, H*D).
+
+    Both qk_prep calls write into one (B, H, L_txt + L_img, D) buffer at their sequence
+    offsets, which replaces the reference's three concatenations."""
+    batch, num_txt, width = txt_qkv.shape
+    num_img = img_qkv.shape[1]
+    head_dim = width // (3 * num_heads)
+    shape = (batch, num_heads, num_txt + num_img, head_dim)
+    joint = tuple(torch.empty(shape, dtype=torch.bfloat16, device=txt_qkv.device) for _ in range(3))
+    qkv_prep(txt_qkv, *txt_scales, None, _slice(freqs, 0, num_txt), num_heads, out=joint, out_offset=0)
+    qkv_prep(img_qkv, *img_scales, None, _slice(freqs, num_txt, num_txt + num_img), num_heads,
+             out=joint, out_offset=num_txt)
+    attn = merge_heads(attend(*joint))
+    return attn[:, :num_txt], attn[:, num_txt:]
+
+
+def single_attention(linear1_out, q_scale, k_scale, freqs: Freqs, num_heads: int, hidden: int):
+    """modules.py:185-191 + 198 -- the qkv part of the fused linear1 output (a strided view,
+    consumed without a copy) -> qk prep -> attention -> merge; returns (attn, mlp)."""
+    qkv, mlp = linear1_out[..., : 3 * hidden], linear1_out[..., 3 * hidden:]
+    q, k, v = qkv_prep(qkv, q_scale, k_scale, None, freqs, num_heads)
+    return merge_heads(attend(q, k, v)), mlp

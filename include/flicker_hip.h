@@ -1,0 +1,95 @@
+/*
+ * flicker_hip.h -- C ABI of libflicker_hip.so, the MI355X (gfx950) kernels behind
+ * flicker_amd's drop-in replacements for kelechi-c/flicker's DiT attention hot path.
+ *
+ * Conventions for every entry point:
+ *   - The caller owns every buffer (device memory).  The library allocates nothing,
+ *     keeps no state between calls and never synchronises the host.
+ *   - Work is enqueued on `stream` (a hipStream_t; NULL = the default stream).
+ *   - bf16 tensors are passed as `void*` to raw 16-bit bf16 storage.
+ *   - Return value: FLK_OK (0) on success, a negative FLK_E_* code for an argument
+ *     the kernel cannot take (checked before anything is launched), or a positive
+ *     hipError_t if the launch itself failed.  flk_status_string() names each code.
+ */
+#ifndef FLICKER_HIP_H
+#define FLICKER_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FLK_OK 0
+#define FLK_E_INVALID (-1)     /* a size, count or offset out of range          */
+#define FLK_E_ALIGN (-2)       /* a pointer or stride breaks the 16-byte rule    */
+#define FLK_E_UNSUPPORTED (-3) /* a shape this build has no kernel for          */
+
+/* ABI revision of this header (bumped on any signature change). */
+int flk_abi_version(void);
+
+/* Static, human-readable text for a return code of any entry point. */
+const char* flk_status_string(int status);
+
+/*
+ * Fused head transpose + QK-RMSNorm + multi-axis RoPE.
+ * Replaces kernels.qk_prep (src/flicker/kernels.py:57-91; tile body _body :35-53).
+ *   qkv        (batch, length, 3*num_heads*head_dim) bf16; element (b, t, c) lives at
+ *              qkv + b*qkv_batch_stride + t*qkv_row_stride + c (strides in elements,
+ *              multiples of 8; the last axis contiguous)
+ *   cos, sin   (length, head_dim) float32 lane tables (kernels.lane_pair layout), row t at
+ *              t*table_row_stride floats (multiple of 4)
+ *   q_scale, k_scale (head_dim,) bf16 (scale_is_f32 = 0) or float32 (scale_is_f32 = 1)
+ *   q_gain     multiplies the rotated query before its bf16 rounding (1.0 = none)
+ *   q_out, k_out, v_out  (batch, num_heads, out_length, head_dim) bf16; token t of this call
+ *              is written at sequence index out_offset + t (out_offset + length <= out_length),
+ *              so two calls can fill one concatenated text|image buffer
+ * head_dim must be 128.
+ */
+int flk_qk_prep(const void* qkv, int64_t qkv_batch_stride, int64_t qkv_row_stride,
+                const float* cos, const float* sin, int64_t table_row_stride,
+                const void* q_scale, const void* k_scale, int scale_is_f32, float q_gain,
+                int batch, int length, int num_heads, int head_dim,
+                void* q_out, void* k_out, void* v_out, int64_t out_length, int64_t out_offset,
+                void* stream);
+
+/*
+ * Bounded flash attention: softmax without the running max, legal because the
+ * QK-norm scales bound every logit (checked at load time, kernels.logit_bound).
+ * Replaces kernels.attend (src/flicker/kernels.py:105-145).
+ *   q, k, v, o (batch, heads, length, head_dim) bf16, contiguous; q is already scaled by
+ *   1/sqrt(head_dim).  o = bf16(sum_j bf16(exp(q.k_j)) v_j / sum_j f32(bf16(exp(q.k_j)))).
+ * Any length >= 1 (tail tiles are masked).  head_dim must be 128.
+ */
+int flk_attend(const void* q, const void* k, const void* v, void* o,
+               int batch, int heads, int length, int head_dim, void* stream);
+
+/*
+ * RoPE angle tables.  Replaces rope.embed_nd / rope.rope_freqs (src/flicker/rope.py:9-21):
+ *   ids  (length, n_axes) float32 positions, row t at t*ids_row_stride floats
+ *   axes_dim  host array of n_axes even ints (1 <= n_axes <= 8)
+ *   pe   (length, P, 2, 2) float32 with P = sum(axes_dim)/2: [[cos, -sin], [sin, cos]] of
+ *        angle = id * theta^(-2k/dim) for pair k of each axis, axes concatenated in order.
+ */
+int flk_rope_embed(const float* ids, int64_t ids_row_stride, int64_t length, int n_axes,
+                   const int* axes_dim, float theta, float* pe, void* stream);
+
+/*
+ * Lane tables from a pe table.  Replaces kernels.lane_pair (src/flicker/kernels.py:28-31):
+ *   pe (length, pairs, 2, 2) float32 -> cos, sin (length, 2*pairs) float32 with
+ *   cos[t,2j] = cos[t,2j+1] = pe[t,j,0,0], sin[t,2j] = -pe[t,j,1,0], sin[t,2j+1] = pe[t,j,1,0].
+ */
+int flk_lane_pair(const float* pe, int64_t length, int pairs, float* cos, float* sin, void* stream);
+
+/*
+ * flk_rope_embed followed by flk_lane_pair in one pass (no pe table in memory).
+ * Produces the same cos/sin tables as kernels.lane_pair(rope.embed_nd(ids)).
+ */
+int flk_rope_lanes(const float* ids, int64_t ids_row_stride, int64_t length, int n_axes,
+                   const int* axes_dim, float theta, float* cos, float* sin, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FLICKER_HIP_H */

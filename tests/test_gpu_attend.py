@@ -1,0 +1,109 @@
+"""attend on the GPU (flk_attend) against the CPU restatement of kernels.py:105-145.
+
+Two gates:
+  * tight, against the bounded-attention restatement (same P rounding, same l):
+    max |diff| <= 2 bf16 ulps of the largest output plus at most 1% of elements off;
+  * the path's tolerance against the plain-XLA restatement (nn.py:35-44):
+    max-abs <= 2e-2 and mean-abs <= 2e-3 on the bf16 output.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from flicker_amd import kernels
+from oracle import path as P
+from tests._util import abs_stats, describe, to_np
+
+pytestmark = pytest.mark.gpu
+D = 128
+MAX_ABS, MEAN_ABS = 2e-2, 2e-3
+
+
+def prepped_case(batch, heads, length, seed, scale=1.0):
+    """q, k, v as qk_prep makes them: unit-RMS rows * scale, q pre-scaled by 1/sqrt(D)."""
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(3, batch, heads, length, D, generator=g)
+    x = x / x.pow(2).mean(-1, keepdim=True).sqrt()
+    q = (x[0] * scale / math.sqrt(D)).to(torch.bfloat16)
+    k = (x[1] * scale).to(torch.bfloat16)
+    v = torch.randn(batch, heads, length, D, generator=g).to(torch.bfloat16)
+    return q, k, v
+
+
+def run_attend(q, k, v, device):
+    q, k, v = (t.to(device) for t in (q, k, v))
+    out = torch.empty_like(q)
+    kernels._launch_attend(q.contiguous(), k.contiguous(), v.contiguous(), out)
+    torch.cuda.synchronize()
+    return to_np(out)
+
+
+def tight_gate(label, got, want):
+    diff = np.abs(got.astype(np.float64) - want)
+    scale = float(np.abs(want).max())
+    ulp = 2.0 ** (math.floor(math.log2(scale)) - 7)
+    st = {"max_abs": float(diff.max()), "mean_abs": float(diff.mean()),
+          "max_ulps_of_max": float(diff.max() / ulp), "mismatch": float(np.mean(diff > 0))}
+    print(describe(label, st))
+    assert st["max_ulps_of_max"] <= 2.0, st
+    assert st["mismatch"] <= 0.01, st
+
+
+@pytest.mark.parametrize("batch,heads,length", [
+    (1, 2, 64), (1, 2, 128), (2, 3, 1536), (1, 2, 4352),
+    (1, 1, 1), (1, 2, 63), (1, 2, 65), (1, 2, 100), (1, 2, 257),
+])
+def test_attend_matches_bounded_oracle(device, batch, heads, length):
+    q, k, v = prepped_case(batch, heads, length, seed=length)
+    got = run_attend(q, k, v, device)
+    want = P.attend_bounded(to_np(q), to_np(k), to_np(v))
+    tight_gate(f"B{batch} H{heads} L{length}", got, want)
+
+
+def test_attend_peaked_logits(device):
+    """Large norm scales (bound 11.3 * 2.4^2 = 65 < 80): far-from-uniform attention."""
+    q, k, v = prepped_case(1, 2, 512, seed=5, scale=2.4)
+    got = run_attend(q, k, v, device)
+    want = P.attend_bounded(to_np(q), to_np(k), to_np(v))
+    tight_gate("peaked", got, want)
+
+
+def test_attend_uniform_keys_give_mean_of_values(device):
+    """All keys equal -> every weight is 1/L -> o = mean(v) (rounded to bf16)."""
+    q, k, v = prepped_case(1, 2, 256, seed=6)
+    k = k[:, :, :1].expand_as(k).contiguous()
+    got = run_attend(q, k, v, device)
+    mean_v = to_np(v).astype(np.float64).mean(axis=2, keepdims=True)
+    st = abs_stats(got, np.broadcast_to(mean_v, got.shape))
+    print(describe("uniform keys", st))
+    assert st["max_abs"] <= 2e-3
+
+
+def test_attend_dominant_key_selects_its_value(device):
+    """One key aligned with the query at logit ~ 60 outweighs 255 others at ~0."""
+    length = 256
+    q = torch.zeros(1, 1, length, D)
+    q[..., 0] = 60.0 / math.sqrt(D) / 4          # q . k_0 = 60
+    k = torch.zeros(1, 1, length, D)
+    k[:, :, 7, 0] = 4 * math.sqrt(D)
+    g = torch.Generator().manual_seed(8)
+    v = torch.randn(1, 1, length, D, generator=g)
+    q, k, v = (t.to(torch.bfloat16) for t in (q, k, v))
+    got = run_attend(q, k, v, device)
+    want = np.broadcast_to(to_np(v)[:, :, 7:8], got.shape)
+    st = abs_stats(got, want)
+    print(describe("dominant key", st))
+    assert st["max_abs"] <= 1e-2
+
+
+def test_attend_python_api_errors(device):
+    q, k, v = (t.to(device) for t in prepped_case(1, 1, 100, seed=1))
+    with pytest.raises(StopIteration):
+        kernels.attend(q, k, v)                 # no score tile divides 100, as in the reference
+    with pytest.raises(ValueError):
+        kernels.attend(q, k, v, block=64)
+    with pytest.raises(ValueError):
+        kernels.attend(q, k, v, interpret=True)

@@ -1,0 +1,157 @@
+"""qk_prep on the GPU (flk_qk_prep) against the CPU restatement of kernels.py:35-91.
+
+Gate: v is a bit-exact copy.  For q and k at most 0.01% of elements may differ from the
+oracle, and each difference must be explainable by one intermediate bf16 rounding
+landing one ulp apart: the oracle's mean of squares is exact while the kernel's is a
+float32 tree sum, so bf16(x * rsqrt(ms + eps)) can flip by an ulp on a rounding tie;
+the rotation then carries that flip into both outputs of the pair.  Bound per element:
+gain * 2 * (ulp(y_i) + ulp(y_pair)) + ulp(out_i), y = the normed-and-scaled input.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from flicker_amd import kernels, modules
+from oracle import path as P
+from oracle.numerics import bf16_ulp
+from tests._util import describe, to_np, ulp_stats
+
+pytestmark = pytest.mark.gpu
+D = 128
+
+
+def make_case(batch, length, heads, seed, scale_dtype=torch.bfloat16, scale_sd=0.05):
+    g = torch.Generator().manual_seed(seed)
+    qkv = torch.randn(batch, length, 3 * heads * D, generator=g).to(torch.bfloat16)
+    qs = (1 + scale_sd * torch.randn(D, generator=g)).to(scale_dtype)
+    ks = (1 + scale_sd * torch.randn(D, generator=g)).to(scale_dtype)
+    ids = torch.randint(0, 128, (length, 4), generator=g).float().numpy()
+    return qkv, qs, ks, ids
+
+
+def oracle_tables(ids, gain):
+    return P.lane_pair(P.embed_nd(ids), gain)
+
+
+def gpu_freqs(tables, device):
+    return kernels.Freqs(torch.from_numpy(tables.cos).to(device), torch.from_numpy(tables.sin).to(device),
+                         tables.q_gain)
+
+
+def check_qkv(label, got, want, gain):
+    """want = qk_prep_fused(..., return_normed=True) output: (q, k, v, yq, yk)."""
+    gq, gk, gv = (to_np(t) for t in got)
+    wq, wk, wv, yq, yk = want
+    assert np.array_equal(gv, wv), f"{label}: v is not a bit-exact copy"
+    for name, g, w, y, gn in (("q", gq, wq, yq, gain), ("k", gk, wk, yk, 1.0)):
+        st = ulp_stats(g, w)
+        ulp_y = bf16_ulp(y)
+        ulp_pair = np.empty_like(ulp_y)
+        ulp_pair[..., 0::2], ulp_pair[..., 1::2] = ulp_y[..., 1::2], ulp_y[..., 0::2]
+        bound = np.float32(gn) * 2 * (ulp_y + ulp_pair) + bf16_ulp(w)
+        excess = float((np.abs(g.astype(np.float64) - w) / bound).max())
+        print(describe(f"{label} {name}", st), f"diff/bound={excess:.3g}")
+        assert st["mismatch"] <= 1e-4, f"{label} {name}: {st}"
+        assert excess <= 1.0, f"{label} {name}: a difference exceeds one intermediate ulp flip ({excess})"
+
+
+@pytest.mark.parametrize("batch,length,heads,gain", [
+    (1, 64, 24, 1 / math.sqrt(128)),
+    (2, 128, 24, 1.0),
+    (1, 1536, 24, 1 / math.sqrt(128)),
+    (3, 256, 6, 0.5),
+    (1, 512, 5, 1 / math.sqrt(128)),
+])
+def test_qk_prep_matches_oracle(device, batch, length, heads, gain):
+    qkv, qs, ks, ids = make_case(batch, length, heads, seed=length + heads)
+    tables = oracle_tables(ids, gain)
+    got = kernels.qk_prep(qkv.to(device), qs.to(device), ks.to(device), gpu_freqs(tables, device), heads)
+    torch.cuda.synchronize()
+    want = P.qk_prep_fused(to_np(qkv), to_np(qs), to_np(ks), tables, heads, return_normed=True)
+    check_qkv(f"B{batch} L{length} H{heads} gain{gain:.4f}", got, want, gain)
+
+
+@pytest.mark.parametrize("length", [1, 17, 100, 4352])
+def test_qk_prep_ragged_length(device, length):
+    """Lengths that are not multiples of the 16-token block (through qkv_prep, which has no
+    row-tile condition, as the reference's plain branch)."""
+    qkv, qs, ks, ids = make_case(1, length, 24, seed=length)
+    tables = oracle_tables(ids, 1.0)
+    got = modules.qkv_prep(qkv.to(device), qs.to(device), ks.to(device), None,
+                           gpu_freqs(tables, device), 24)
+    torch.cuda.synchronize()
+    check_qkv(f"L{length}", got, P.qk_prep_fused(to_np(qkv), to_np(qs), to_np(ks), tables, 24,
+                                                return_normed=True), 1.0)
+
+
+def test_qk_prep_f32_scales(device):
+    qkv, qs, ks, ids = make_case(1, 128, 24, seed=7, scale_dtype=torch.float32)
+    tables = oracle_tables(ids, 1 / math.sqrt(128))
+    got = kernels.qk_prep(qkv.to(device), qs.to(device), ks.to(device), gpu_freqs(tables, device), 24)
+    torch.cuda.synchronize()
+    want = P.qk_prep_fused(to_np(qkv), to_np(qs), to_np(ks), tables, 24, scale_is_bf16=False,
+                           return_normed=True)
+    check_qkv("f32 scales", got, want, tables.q_gain)
+
+
+def test_qk_prep_gain_one_equals_plain_path(device):
+    """At q_gain = 1 the fused kernel computes the plain-XLA branch (modules.py:78-80)."""
+    qkv, qs, ks, ids = make_case(2, 256, 24, seed=11)
+    pe = P.embed_nd(ids)
+    got = modules.qkv_prep(qkv.to(device), qs.to(device), ks.to(device), torch.from_numpy(pe).to(device),
+                           None, 24)
+    torch.cuda.synchronize()
+    plain = P.qk_prep_plain(to_np(qkv), to_np(qs), to_np(ks), pe, 24)
+    fused = P.qk_prep_fused(to_np(qkv), to_np(qs), to_np(ks), P.lane_pair(pe, 1.0), 24, return_normed=True)
+    assert all(np.array_equal(a, b) for a, b in zip(plain, fused[:3]))
+    check_qkv("plain", got, plain + fused[3:], 1.0)
+
+
+def test_qk_prep_strided_single_block_view(device):
+    """The qkv part of a single block's fused linear1 output (modules.py:185-189), as a view."""
+    length, heads = 256, 24
+    g = torch.Generator().manual_seed(3)
+    lin1 = torch.randn(1, length, 3 * heads * D + 2 * 9216, generator=g).to(torch.bfloat16)
+    _, qs, ks, ids = make_case(1, length, heads, seed=4)
+    tables = oracle_tables(ids, 1 / math.sqrt(128))
+    dev = lin1.to(device)
+    view = dev[..., : 3 * heads * D]
+    assert not view.is_contiguous()
+    got = kernels.qk_prep(view, qs.to(device), ks.to(device), gpu_freqs(tables, device), heads)
+    torch.cuda.synchronize()
+    want = P.qk_prep_fused(to_np(lin1)[..., : 3 * heads * D], to_np(qs), to_np(ks), tables, heads,
+                           return_normed=True)
+    check_qkv("strided", got, want, tables.q_gain)
+
+
+def test_qk_prep_out_offset_fills_joint_buffer(device):
+    """Text and image streams written at their offsets equal separate calls concatenated."""
+    heads, n_txt, n_img = 24, 512, 256
+    txt, qs_t, ks_t, ids_t = make_case(1, n_txt, heads, seed=21)
+    img, qs_i, ks_i, ids_i = make_case(1, n_img, heads, seed=22)
+    ft = gpu_freqs(oracle_tables(ids_t, 0.125), device)
+    fi = gpu_freqs(oracle_tables(ids_i, 0.125), device)
+    joint = tuple(torch.full((1, heads, n_txt + n_img, D), float("nan"), dtype=torch.bfloat16, device=device)
+                  for _ in range(3))
+    kernels.qk_prep(txt.to(device), qs_t.to(device), ks_t.to(device), ft, heads, out=joint, out_offset=0)
+    kernels.qk_prep(img.to(device), qs_i.to(device), ks_i.to(device), fi, heads, out=joint, out_offset=n_txt)
+    sep_t = kernels.qk_prep(txt.to(device), qs_t.to(device), ks_t.to(device), ft, heads)
+    sep_i = kernels.qk_prep(img.to(device), qs_i.to(device), ks_i.to(device), fi, heads)
+    torch.cuda.synchronize()
+    for j, a, b in zip(joint, sep_t, sep_i):
+        assert torch.equal(j, torch.cat([a, b], dim=2))
+
+
+def test_qk_prep_klein_1024_full(device):
+    """The headline shape: (1, 4608, 9216) with the workload's own tables and scales."""
+    from flicker_amd import workloads
+    w = workloads.WORKLOADS["klein_1024"]
+    qkv, (qs, ks), ids = workloads.make_qkv(w), workloads.make_scales(w), workloads.make_ids(w)
+    tables = oracle_tables(ids, workloads.q_gain(w))
+    got = kernels.qk_prep(qkv.to(device), qs.to(device), ks.to(device), gpu_freqs(tables, device), 24)
+    torch.cuda.synchronize()
+    check_qkv("klein_1024", got, P.qk_prep_fused(to_np(qkv), to_np(qs), to_np(ks), tables, 24,
+                                                  return_normed=True), tables.q_gain)
