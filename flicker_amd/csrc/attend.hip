@@ -7,124 +7,218 @@
 //   l += f32(P);  acc += P * v_j                       (f32)
 //   o_i = bf16(acc / l)
 //
-// Formulation.  Each wave owns 32 queries and computes the transposed score tile
-// S^T = K Q^T with v_mfma_f32_32x32x16_bf16 (A = K rows from LDS, B = Q^T held in
-// registers for the whole kernel).  In the 32x32 accumulator layout a lane owns one
-// query column and 16 key rows, so
+// Formulation.  Each wave owns 64 queries (two 32-query column blocks) and computes the
+// transposed score tile S^T = K Q^T with v_mfma_f32_32x32x16_bf16 (A = K rows from LDS,
+// B = Q^T held in registers for the whole kernel).  In the 32x32 accumulator layout a
+// lane owns one query column and 16 key rows, so
 //   * exp / bf16 rounding / the row sum l are lane-local (l is reduced across the two
 //     lane halves once, in the epilogue), and
 //   * the rounded P registers are directly the B operand (keys x queries) of the second
 //     product O^T += V^T P^T -- no shuffle of P through LDS.
-// V^T is the A operand of that product, so V tiles are written to LDS transposed
-// (d-major) during staging, with the key order inside each 16-key group permuted to
-// match the accumulator-row order of S^T, so one ds_read_b128 fetches an operand.
+// Every LDS operand read feeds two MFMAs (one per query block).  V stays row-major in
+// LDS; its transposed operand (d rows x 8 keys per lane) is fetched with two
+// ds_read_b64_tr_b16, whose 16-lane transpose hands lane 4a+b element b of source lanes
+// a, a+4, a+8, a+12 -- so source lane s points at key K0 + s/4, columns D0 + 4(s%4).
+// The 8 keys a lane receives follow the accumulator-row order of S^T, so the P
+// registers of lane half g line up with the V^T k-slots of the same half.
 //
-// Staging: a 256-thread block (4 waves, 128 queries) streams 64-key K and V tiles
-// through two LDS buffers: the next tile's global loads are issued before the current
-// tile's MFMAs and written to the other buffer after them (one barrier per tile).
-// LDS rows are XOR-swizzled in 16-byte chunks so the operand reads of 16 consecutive
-// lanes hit distinct banks.  Blocks are renumbered so that all query tiles of one head
-// run on the same XCD (hardware deals blocks round-robin over the 8 XCDs), keeping
-// that head's K/V resident in one L2.
+// Staging.  K and V tiles (64 keys x 256 B each) go from global memory straight into
+// LDS with global_load_lds_dwordx4 (no registers): lane i of a wave instruction lands
+// at base + 16 i, so the XOR swizzle is applied by choosing which global chunk each
+// lane fetches.  Both tiles use chunk' = chunk ^ swz(row), swz = ((row&3)<<1)|((row>>2)&1),
+// which keeps every 8 consecutive K rows (b128 operand reads) and every group of 4 V
+// rows x 2 chunks (transpose reads) on distinct banks of the 32-bank LDS.
+//
+// Pipeline.  A 256-thread block (4 waves = one per SIMD, 256 queries) streams tiles
+// through a 3-buffer ring, two 32-key units per tile.  In the phase of unit u the wave
+// first issues all 16 LDS operand reads, then alternates each QK^T MFMA of unit u+1
+// with the exp / bf16 / row-sum VALU work of two elements of unit u (explicit schedule
+// fences keep that interleave), then runs the 16 PV MFMAs of unit u.  The copy of tile
+// t+2 is issued in tile t's second phase and waited on before the tile's closing barrier.
+// Blocks are renumbered so that all query tiles of one head run on the same XCD
+// (hardware deals blocks round-robin over the 8 XCDs), keeping the head's K/V in one L2.
 
 #include "common.h"
 
 namespace {
 
 constexpr int kD = 128;                 // head dim
-constexpr int kWaves = 4;
-constexpr int kQW = 32;                 // queries per wave
-constexpr int kBM = kWaves * kQW;       // queries per block
-constexpr int kBN = 64;                 // keys per tile
+#ifndef FLK_ATTEND_WAVES
+#define FLK_ATTEND_WAVES 8
+#endif
+#ifndef FLK_ATTEND_QB
+#define FLK_ATTEND_QB 1
+#endif
+constexpr int kWaves = FLK_ATTEND_WAVES;   // waves per block (two per SIMD at 8)
+constexpr int kQB = FLK_ATTEND_QB;         // 32-query column blocks per wave
+constexpr int kWavesPerSimd = kWaves / 4;
+constexpr int kRowsPerWave = 64 / kWaves;  // tile rows each wave copies
+constexpr int kBM = kWaves * kQB * 32;  // queries per block
+constexpr int kBN = 64;                 // keys per LDS tile (two 32-key units)
+constexpr int kStages = 3;
 constexpr int kThreads = kWaves * 64;
-constexpr int kKBytes = kBN * kD * 2;   // K tile: kBN rows x 256 B
-constexpr int kVBytes = kD * kBN * 2;   // V^T tile: kD rows x 128 B
-constexpr int kBufBytes = kKBytes + kVBytes;
+constexpr int kRowBytes = kD * 2;       // one K or V row: 256 B = 16 chunks of 16 B
+constexpr int kTileBytes = kBN * kRowBytes;
+constexpr int kBufBytes = 2 * kTileBytes;  // K tile then V tile
+constexpr int kUnitBytes = 32 * kRowBytes;
 constexpr int kXcds = 8;
 constexpr float kLog2e = 1.4426950408889634f;
 
+using flk::bf16x2;
 using flk::bf16x8;
 using flk::f32x16;
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x8 __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
-// Chunk swizzle of a 128-byte V^T row (8 chunks of 16 B): conflict-free for 16 consecutive
-// rows on 64 banks and for 8 consecutive rows on 32 banks.
-__device__ __forceinline__ int vt_swizzle(int d) { return (d & 7) ^ ((d >> 3) & 1); }
+__device__ __forceinline__ int swz(int row) { return ((row & 3) << 1) | ((row >> 2) & 1); }
 
-// Position of tile key `kappa` (0..63) inside its V^T row: chunk (before swizzle) and
-// byte offset inside the chunk.  Slot (g, j) of the PV operand at key step ks holds key
-// ks*16 + (j/4)*8 + g*4 + j%4, the key that S^T accumulator register 8*(ks%2)+j of lane
-// half g holds.
-__device__ __forceinline__ void vt_slot(int kappa, int& chunk, int& byte_in_chunk) {
-  const int ks = kappa >> 4, r = kappa & 15;
-  chunk = ks * 2 + ((r >> 2) & 1);
-  byte_in_chunk = (((r >> 3) << 2) + (r & 3)) * 2;
+// Copy one 64-key tile of K and V (rows kv0..kv0+63, clamped to the last row) into `buf`.
+// Each wave moves 64/kWaves rows of K and of V, 4 rows (64 lanes x 16 B) per instruction.
+__device__ __forceinline__ void copy_tile(uint8_t* buf, const uint16_t* __restrict__ kh,
+                                          const uint16_t* __restrict__ vh, int kv0, int length,
+                                          int wave, int lane) {
+#pragma unroll
+  for (int i = 0; i < kRowsPerWave / 4; ++i) {
+    const int row0 = wave * kRowsPerWave + i * 4;               // wave-uniform first row
+    const int row = row0 + (lane >> 4);                          // tile row this lane fills
+    const int chunk = (lane & 15) ^ swz(row);                    // logical chunk for its slot
+    const int key = min(kv0 + row, length - 1);
+    const int64_t src = (int64_t)key * kD + chunk * 8;
+    const int dst = row0 * kRowBytes;
+    __builtin_amdgcn_global_load_lds(kh + src, (lds_void*)(buf + dst), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(vh + src, (lds_void*)(buf + kTileBytes + dst), 16, 0, 0);
+  }
 }
 
-struct Tile {
-  uint4 k[4];
-  uint4 v[4];
+struct WaveState {
+  bf16x8 qreg[kQB][8];
+  f32x16 oacc[kQB][4];
+  f32x16 sA[kQB];
+  f32x16 sB[kQB];
+  float lsum[kQB];
+  int k_off[8];   // K operand byte offsets within a unit (d step st)
+  int v_off[4];   // V^T transpose-read byte offsets within a tile (d block m), key step 0
 };
 
-__device__ __forceinline__ void load_tile(Tile& tl, const uint16_t* __restrict__ kh,
-                                          const uint16_t* __restrict__ vh, int kv0, int length,
-                                          int kg, int ch) {
+__device__ __forceinline__ bf16x8 v_operand(const uint8_t* vtile, int off) {
+  const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vtile + off));
+  const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vtile + off + 8 * kRowBytes));
+  const s16x8 both = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+  return __builtin_bit_cast(bf16x8, both);
+}
+
+// exp / bf16 / row-sum of one element pair (two keys of one query).
+template <bool kMask>
+__device__ __forceinline__ uint32_t exp_pair(float s0, float s1, float& lsum, int key0, int length) {
+  float e0 = __builtin_amdgcn_exp2f(s0 * kLog2e);
+  float e1 = __builtin_amdgcn_exp2f(s1 * kLog2e);
+  if constexpr (kMask) {
+    e0 = key0 < length ? e0 : 0.0f;
+    e1 = key0 + 1 < length ? e1 : 0.0f;
+  }
+  const uint32_t w = flk::pack_bf16x2(e0, e1);
+  const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
+  lsum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w), ones, lsum, false);
+  return w;
+}
+
+// Unit phase: P(u) = exp(S(u)) interleaved with S(u+1) = K(u+1) Q^T, then O^T += V(u)^T P(u)^T.
+struct TileCopy {
+  uint8_t* dst;        // buffer to fill, or nullptr for none
+  const uint16_t* kh;
+  const uint16_t* vh;
+  int kv0, length, wave, lane;
+};
+
+template <bool kMask>
+__device__ __forceinline__ void unit_phase(WaveState& w, const f32x16 (&s_cur)[kQB],
+                                           f32x16 (&s_next)[kQB], const uint8_t* k_next,
+                                           const uint8_t* v_tile, int ks0, int key_base,
+                                           int length, int g, const TileCopy& copy) {
+  bf16x8 kop[8], vop[2][4];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int key = kv0 + kg * 4 + r;
-    if (key < length) {
-      const int64_t off = (int64_t)key * kD + ch * 8;
-      tl.k[r] = *reinterpret_cast<const uint4*>(kh + off);
-      tl.v[r] = *reinterpret_cast<const uint4*>(vh + off);
-    } else {
-      tl.k[r] = make_uint4(0, 0, 0, 0);
-      tl.v[r] = make_uint4(0, 0, 0, 0);
+  for (int st = 0; st < 8; ++st) kop[st] = *reinterpret_cast<const bf16x8*>(k_next + w.k_off[st]);
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+    for (int m = 0; m < 4; ++m) vop[ks][m] = v_operand(v_tile, w.v_off[m] + (ks0 + ks) * 16 * kRowBytes);
+  // S(u) may sit in accumulation registers (the MFMA wrote it there); moving it to VGPRs
+  // once here, with an empty asm that must see it in VGPRs, keeps the exp work below from
+  // reading accumulation registers element by element while the next MFMAs are in flight,
+  // which serialises each read behind the matrix pipe.
+  f32x16 sv[kQB];
+#pragma unroll
+  for (int qb = 0; qb < kQB; ++qb) {
+    sv[qb] = s_cur[qb];
+    asm volatile("" : "+v"(sv[qb]));
+  }
+  // The next tile copy is issued only after this tile's last operand reads: a pending copy
+  // into LDS makes the compiler wait for it before any later LDS read it cannot prove
+  // disjoint, and the only later reads are behind the tile's closing wait anyway.
+  if (copy.dst) copy_tile(copy.dst, copy.kh, copy.vh, copy.kv0, copy.length, copy.wave, copy.lane);
+  __builtin_amdgcn_sched_barrier(0);
+
+  uint32_t p[kQB][8];
+#pragma unroll
+  for (int qb = 0; qb < kQB; ++qb) s_next[qb] = f32x16{};
+#pragma unroll
+  for (int st = 0; st < 8; ++st) {
+#pragma unroll
+    for (int qb = 0; qb < kQB; ++qb) {
+      s_next[qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop[st], w.qreg[qb][st], s_next[qb], 0, 0, 0);
+      const int i = 2 * st;  // elements i, i+1 of this query block
+      p[qb][st] = exp_pair<kMask>(sv[qb][i], sv[qb][i + 1], w.lsum[qb],
+                                  key_base + (i >> 2) * 8 + g * 4 + (i & 3), length);
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
-}
-
-__device__ __forceinline__ uint32_t lo_pair(uint32_t a, uint32_t b) {
-  return (a & 0xFFFFu) | (b << 16);
-}
-__device__ __forceinline__ uint32_t hi_pair(uint32_t a, uint32_t b) {
-  return (a >> 16) | (b & 0xFFFF0000u);
-}
-
-__device__ __forceinline__ void store_tile(const Tile& tl, uint8_t* buf, int kg, int ch) {
-  uint8_t* ks = buf;
-  uint8_t* vt = buf + kKBytes;
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int key = kg * 4 + r;
-    *reinterpret_cast<uint4*>(ks + key * 256 + ((ch ^ (key & 15)) << 4)) = tl.k[r];
-  }
-  // Transpose: 4 keys (kg*4 .. +3, contiguous in the permuted slot order) x 8 d values.
-  int chunk, byte_in_chunk;
-  vt_slot(kg * 4, chunk, byte_in_chunk);
-  const uint32_t w0[4] = {tl.v[0].x, tl.v[0].y, tl.v[0].z, tl.v[0].w};
-  const uint32_t w1[4] = {tl.v[1].x, tl.v[1].y, tl.v[1].z, tl.v[1].w};
-  const uint32_t w2[4] = {tl.v[2].x, tl.v[2].y, tl.v[2].z, tl.v[2].w};
-  const uint32_t w3[4] = {tl.v[3].x, tl.v[3].y, tl.v[3].z, tl.v[3].w};
+  for (int ks = 0; ks < 2; ++ks) {
+    bf16x8 b[kQB];
 #pragma unroll
-  for (int jj = 0; jj < 8; ++jj) {
-    const int d = ch * 8 + jj;
-    const int w = jj >> 1;
-    uint2 val;
-    if (jj & 1) {
-      val.x = hi_pair(w0[w], w1[w]);
-      val.y = hi_pair(w2[w], w3[w]);
-    } else {
-      val.x = lo_pair(w0[w], w1[w]);
-      val.y = lo_pair(w2[w], w3[w]);
-    }
-    *reinterpret_cast<uint2*>(vt + d * 128 + ((chunk ^ vt_swizzle(d)) << 4) + byte_in_chunk) = val;
+    for (int qb = 0; qb < kQB; ++qb)
+      b[qb] = __builtin_bit_cast(bf16x8, make_uint4(p[qb][ks * 4], p[qb][ks * 4 + 1],
+                                                    p[qb][ks * 4 + 2], p[qb][ks * 4 + 3]));
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+      for (int qb = 0; qb < kQB; ++qb)
+        w.oacc[qb][m] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vop[ks][m], b[qb], w.oacc[qb][m], 0, 0, 0);
   }
 }
 
-__global__ __launch_bounds__(kThreads, 2) void attend_kernel(
+// One 64-key tile = two unit phases.  The second phase computes S of the next tile's first
+// unit (on the last tile it reads a stale buffer; that result is unused) and issues the
+// copy of tile t + 2 into the third buffer.
+template <bool kMask>
+__device__ __forceinline__ void tile_step(WaveState& w, const uint8_t* cur, const uint8_t* nxt,
+                                          int kv0, int length, int g, const TileCopy& copy) {
+  const TileCopy none = {nullptr, nullptr, nullptr, 0, 0, 0, 0};
+  unit_phase<kMask>(w, w.sA, w.sB, cur + kUnitBytes, cur + kTileBytes, 0, kv0, length, g, none);
+  __builtin_amdgcn_sched_barrier(0);
+  unit_phase<kMask>(w, w.sB, w.sA, nxt, cur + kTileBytes, 2, kv0 + 32, length, g, copy);
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+__device__ __forceinline__ void qk_first(WaveState& w, const uint8_t* kunit) {
+#pragma unroll
+  for (int qb = 0; qb < kQB; ++qb) w.sA[qb] = f32x16{};
+#pragma unroll
+  for (int st = 0; st < 8; ++st) {
+    const bf16x8 a = *reinterpret_cast<const bf16x8*>(kunit + w.k_off[st]);
+#pragma unroll
+    for (int qb = 0; qb < kQB; ++qb)
+      w.sA[qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, w.qreg[qb][st], w.sA[qb], 0, 0, 0);
+  }
+}
+
+__global__ __launch_bounds__(kThreads, kWavesPerSimd) void attend_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, uint16_t* __restrict__ o, int length, int q_blocks,
     int total_blocks) {
-  __shared__ __attribute__((aligned(16))) uint8_t smem[2 * kBufBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[kStages * kBufBytes];
 
   // XCD-aware renumbering: hardware block id p runs on XCD p % 8; give each XCD a
   // contiguous range of logical ids (head-major), so a head's query tiles share an L2.
@@ -133,7 +227,7 @@ __global__ __launch_bounds__(kThreads, 2) void attend_kernel(
   const int per = total_blocks / kXcds, extra = total_blocks % kXcds;
   const int logical = xcd * per + min(xcd, extra) + local;
   const int bh = logical / q_blocks;
-  const int qb = logical - bh * q_blocks;
+  const int qblk = logical - bh * q_blocks;
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -146,107 +240,81 @@ __global__ __launch_bounds__(kThreads, 2) void attend_kernel(
   const uint16_t* kh = k + head_off;
   const uint16_t* vh = v + head_off;
 
-  // Q^T operand registers: query qi, d = 16*s + 8*g + j.
-  const int qi = qb * kBM + wave * kQW + c;
-  bf16x8 qreg[8];
-#pragma unroll
-  for (int s = 0; s < 8; ++s) {
-    if (qi < length) {
-      qreg[s] = *reinterpret_cast<const bf16x8*>(qh + (int64_t)qi * kD + s * 16 + g * 8);
-    } else {
-      qreg[s] = bf16x8{};
-    }
-  }
-
-  f32x16 oacc[4];
-#pragma unroll
-  for (int m = 0; m < 4; ++m) oacc[m] = f32x16{};
-  float lsum = 0.0f;
-
-  const int kg = tid >> 4, ch = tid & 15;  // staging role: keys kg*4..+3, 16-byte chunk ch
   const int ntiles = (length + kBN - 1) / kBN;
+  const int full_tiles = length / kBN;
+  copy_tile(smem, kh, vh, 0, length, wave, lane);
+  copy_tile(smem + kBufBytes, kh, vh, kBN, length, wave, lane);
 
-  // Per-lane LDS operand offsets (loop invariant).
-  int k_off[8];
+  WaveState w;
+  const int q0 = qblk * kBM + wave * (kQB * 32);
 #pragma unroll
-  for (int s = 0; s < 8; ++s) k_off[s] = c * 256 + ((((s << 1) | g) ^ (c & 15)) << 4);
-  int v_off[4];
-  const int vsw = vt_swizzle(c);  // same for rows c + 32*m
-#pragma unroll
-  for (int ks = 0; ks < 4; ++ks) v_off[ks] = c * 128 + (((ks << 1) | g) ^ vsw) * 16;
-
-  Tile tl;
-  load_tile(tl, kh, vh, 0, length, kg, ch);
-  store_tile(tl, smem, kg, ch);
-  __syncthreads();
-
-  for (int t = 0; t < ntiles; ++t) {
-    const int kv0 = t * kBN;
-    uint8_t* cur = smem + (t & 1) * kBufBytes;
-    if (t + 1 < ntiles) load_tile(tl, kh, vh, kv0 + kBN, length, kg, ch);
-
-    // S^T = K Q^T for two 32-key halves of the tile.
-    f32x16 sacc[2] = {f32x16{}, f32x16{}};
+  for (int qb = 0; qb < kQB; ++qb) {
+    const int qi = q0 + qb * 32 + c;
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        const bf16x8 a = *reinterpret_cast<const bf16x8*>(cur + kb * 32 * 256 + k_off[s]);
-        sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qreg[s], sacc[kb], 0, 0, 0);
-      }
+      w.qreg[qb][s] = qi < length
+                          ? *reinterpret_cast<const bf16x8*>(qh + (int64_t)qi * kD + s * 16 + g * 8)
+                          : bf16x8{};
     }
-
-    // P = bf16(exp(S)); keys past the end contribute nothing.
-    uint32_t pw[2][8];
-    const bool tail = kv0 + kBN > length;
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-      for (int i = 0; i < 16; i += 2) {
-        float e0 = __builtin_amdgcn_exp2f(sacc[kb][i] * kLog2e);
-        float e1 = __builtin_amdgcn_exp2f(sacc[kb][i + 1] * kLog2e);
-        if (tail) {
-          const int key0 = kv0 + kb * 32 + (i >> 2) * 8 + g * 4 + (i & 3);
-          if (key0 >= length) e0 = 0.0f;
-          if (key0 + 1 >= length) e1 = 0.0f;
-        }
-        const uint32_t packed = flk::pack_bf16x2(e0, e1);
-        pw[kb][i >> 1] = packed;
-        lsum += flk::bf16_lo(packed) + flk::bf16_hi(packed);
-      }
-    }
-
-    // O^T += V^T P^T, 16 keys per MFMA, 4 blocks of 32 d rows.
-    const uint8_t* vt = cur + kKBytes;
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const uint32_t* src = &pw[ks >> 1][(ks & 1) * 4];
-      const uint4 pv = make_uint4(src[0], src[1], src[2], src[3]);
-      const bf16x8 b = __builtin_bit_cast(bf16x8, pv);
-#pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        const bf16x8 a = *reinterpret_cast<const bf16x8*>(vt + m * 32 * 128 + v_off[ks]);
-        oacc[m] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, oacc[m], 0, 0, 0);
-      }
-    }
-
-    if (t + 1 < ntiles) store_tile(tl, smem + ((t + 1) & 1) * kBufBytes, kg, ch);
-    __syncthreads();
+    for (int m = 0; m < 4; ++m) w.oacc[qb][m] = f32x16{};
+    w.lsum[qb] = 0.0f;
   }
-
-  // Epilogue: l over both lane halves, O = bf16(acc / l), rows of 4 d values per store.
-  lsum += __shfl_xor(lsum, 32);
-  if (qi < length) {
-    uint16_t* orow = o + head_off + (int64_t)qi * kD;
+#pragma unroll
+  for (int s = 0; s < 8; ++s) w.k_off[s] = c * kRowBytes + ((((s << 1) | g) ^ swz(c)) << 4);
+  {
+    // Transpose-read source lane: 16-lane block h, lane sl in it -> key g*4 + sl/4 (+16 ks,
+    // +8 for the upper four k-slots), columns m*32 + 16*(h&1) + 4*(sl&3) .. +3.
+    const int h = lane >> 4, sl = lane & 15;
+    const int key = g * 4 + (sl >> 2);
+    const int half = sl & 1;
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
+      const int chunk = 4 * m + 2 * (h & 1) + ((sl & 3) >> 1);
+      w.v_off[m] = key * kRowBytes + ((chunk ^ swz(key)) << 4) + half * 8;
+    }
+  }
+
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  qk_first(w, smem);
+
+  // Full tiles, then the partial tail tile (if any) with key masking.  Tile t lives in
+  // buffer t % 3.  The copy of tile t + 2 is unconditional: past the end it re-reads the
+  // last row into the free buffer.
+  int cur = 0;
+  for (int t = 0; t < full_tiles; ++t) {
+    const int nxt = cur == kStages - 1 ? 0 : cur + 1;
+    const int fill = nxt == kStages - 1 ? 0 : nxt + 1;  // buffer of tile t + 2
+    const TileCopy copy = {smem + fill * kBufBytes, kh, vh, (t + 2) * kBN, length, wave, lane};
+    tile_step<false>(w, smem + cur * kBufBytes, smem + nxt * kBufBytes, t * kBN, length, g, copy);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    cur = nxt;
+  }
+  if (full_tiles < ntiles) {
+    const int nxt = cur == kStages - 1 ? 0 : cur + 1;
+    const TileCopy none = {nullptr, nullptr, nullptr, 0, 0, 0, 0};
+    tile_step<true>(w, smem + cur * kBufBytes, smem + nxt * kBufBytes, full_tiles * kBN, length, g, none);
+  }
+
+  // Epilogue: l over both lane halves, O = bf16(acc / l), 4 d values per 8-byte store.
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int d0 = m * 32 + r * 8 + g * 4;
-        uint2 val;
-        val.x = flk::pack_bf16x2(oacc[m][r * 4 + 0] / lsum, oacc[m][r * 4 + 1] / lsum);
-        val.y = flk::pack_bf16x2(oacc[m][r * 4 + 2] / lsum, oacc[m][r * 4 + 3] / lsum);
-        *reinterpret_cast<uint2*>(orow + d0) = val;
+  for (int qb = 0; qb < kQB; ++qb) {
+    const float l = w.lsum[qb] + __shfl_xor(w.lsum[qb], 32);
+    const int qi = q0 + qb * 32 + c;
+    if (qi < length) {
+      uint16_t* orow = o + head_off + (int64_t)qi * kD;
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int d0 = m * 32 + r * 8 + g * 4;
+          uint2 val;
+          val.x = flk::pack_bf16x2(w.oacc[qb][m][r * 4 + 0] / l, w.oacc[qb][m][r * 4 + 1] / l);
+          val.y = flk::pack_bf16x2(w.oacc[qb][m][r * 4 + 2] / l, w.oacc[qb][m][r * 4 + 3] / l);
+          *reinterpret_cast<uint2*>(orow + d0) = val;
+        }
       }
     }
   }
