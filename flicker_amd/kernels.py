@@ -143,13 +143,13 @@ def qk_prep(qkv: torch.Tensor, q_scale: torch.Tensor, k_scale: torch.Tensor, fre
     (or the default row tile) must divide L; the HIP kernel itself tiles by 16 tokens."""
     if interpret:
         raise ValueError("interpret=True is Pallas' CPU emulation; flicker_amd has one HIP path")
-    _on_gpu("qkv", qkv)
     if qkv.dim() != 3:
         raise ValueError(f"qkv must be (B, L, 3*H*D), got {tuple(qkv.shape)}")
     length = qkv.shape[1]
     tile_rows = rows or row_tile(length)
     if tile_rows is None or length % tile_rows:
         raise ValueError(f"qk_prep needs a row tile dividing L={length} (rows={tile_rows})")
+    _on_gpu("qkv", qkv)
     return _launch_qk_prep(qkv, q_scale, k_scale, freqs, num_heads, out, out_offset)
 
 
@@ -173,19 +173,21 @@ def attend(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, block: int | No
     if interpret:
         raise ValueError("interpret=True is Pallas' CPU emulation; flicker_amd has one HIP path")
     for name, t in (("q", q), ("k", k), ("v", v)):
-        _on_gpu(name, t)
-        if t.dtype != torch.bfloat16:
-            raise TypeError(f"{name} must be bfloat16, got {t.dtype}")
         if t.dim() != 4:
             raise ValueError(f"{name} must be (B, H, L, D), got {tuple(t.shape)}")
     if not (q.shape == k.shape == v.shape):
         raise ValueError(f"q, k, v shapes differ: {tuple(q.shape)} {tuple(k.shape)} {tuple(v.shape)}")
     batch, heads, length, dim = q.shape
+    # as in the reference: no score tile dividing L raises StopIteration (kernels.py:110)
     block = block or next(size for size in SCORE_TILES if length % size == 0)
     if length % block:
         raise ValueError(f"attend block {block} does not divide L={length}")
     if dim != HEAD_DIM:
         raise ValueError(f"attend: head_dim {dim} unsupported (kernels are built for {HEAD_DIM})")
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        _on_gpu(name, t)
+        if t.dtype != torch.bfloat16:
+            raise TypeError(f"{name} must be bfloat16, got {t.dtype}")
     q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
     if out is None:
         out = torch.empty_like(q)

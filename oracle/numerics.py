@@ -14,13 +14,15 @@ _QUIET = np.uint32(0x00400000)
 
 def bf16_round(x) -> np.ndarray:
     """float32 -> nearest bf16 value (ties to even), returned as float32."""
-    x = np.ascontiguousarray(x, dtype=np.float32)
+    x = np.asarray(x, dtype=np.float32)
+    shape = x.shape
+    x = np.ascontiguousarray(x).reshape(-1)
     u = x.view(np.uint32)
     lsb = (u >> np.uint32(16)) & np.uint32(1)
     with np.errstate(over="ignore"):
         r = (u + _ROUND_BIAS + lsb) & _HI_MASK
     r = np.where(np.isnan(x), (u | _QUIET) & _HI_MASK, r)
-    return r.view(np.float32)
+    return r.view(np.float32).reshape(shape)
 
 
 def bf16_bits(x) -> np.ndarray:

@@ -39,6 +39,11 @@ def smooth_factors(x_absmax, w_absmax) -> np.ndarray:
     return s
 
 
+def inverse(s) -> np.ndarray:
+    """inv_s_j = 1 / s_j (f32, correctly rounded): the multiplier applied to activations."""
+    return (F32(1) / np.asarray(s, dtype=F32)).astype(F32)
+
+
 def _quantize(values: np.ndarray, scale: np.ndarray) -> np.ndarray:
     q = np.rint((values / scale).astype(F32))
     return np.clip(q, -QMAX, QMAX).astype(np.int8)

@@ -1,0 +1,179 @@
+"""Host-side checks that need no GPU: the C ABI library loads and exports what the header
+declares, its argument validation rejects bad calls before launching anything, the Python
+boundary raises the reference's errors, and the workload bookkeeping is right."""
+
+import ctypes
+import math
+import os
+import re
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from flicker_amd import _lib, kernels, loader, rope, workloads
+from oracle import path as P
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_symbols():
+    text = open(os.path.join(ROOT, "include", "flicker_hip.h")).read()
+    return sorted(set(re.findall(r"\b(flk_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not _lib.LIB_PATH.exists():
+        pytest.fail(f"{_lib.LIB_PATH} not built: run python -m flicker_amd.build")
+    return _lib.lib()
+
+
+def test_library_exports_every_declared_symbol(lib):
+    syms = declared_symbols()
+    assert syms, "no declarations found in include/flicker_hip.h"
+    assert sorted(_lib.SIGNATURES) == syms
+    for name in syms:
+        assert hasattr(lib, name), name
+    assert lib.flk_abi_version() == _lib.ABI_VERSION
+
+
+def test_status_strings(lib):
+    for code in (_lib.FLK_OK, _lib.FLK_E_INVALID, _lib.FLK_E_ALIGN, _lib.FLK_E_UNSUPPORTED):
+        assert _lib.status_string(code)
+    assert "unsupported" in _lib.status_string(_lib.FLK_E_UNSUPPORTED)
+
+
+FAKE = 0x10000  # a 16-byte aligned, never dereferenced address: every call below fails validation first
+
+
+def test_attend_validation(lib):
+    f = lib.flk_attend
+    assert f(FAKE, FAKE, FAKE, FAKE, 1, 24, 4608, 64, None) == _lib.FLK_E_UNSUPPORTED
+    assert f(FAKE, FAKE, FAKE, FAKE, -1, 24, 4608, 128, None) == _lib.FLK_E_INVALID
+    assert f(FAKE + 8, FAKE, FAKE, FAKE, 1, 24, 4608, 128, None) == _lib.FLK_E_ALIGN
+    assert f(None, FAKE, FAKE, FAKE, 1, 24, 4608, 128, None) == _lib.FLK_E_INVALID
+    assert f(FAKE, FAKE, FAKE, FAKE, 0, 24, 4608, 128, None) == _lib.FLK_OK       # empty: nothing launched
+
+
+def test_qk_prep_validation(lib):
+    f = lib.flk_qk_prep
+    args = dict(qkv=FAKE, bs=4608 * 9216, rs=9216, cos=FAKE, sin=FAKE, ts=128, qs=FAKE, ks=FAKE, f32=0,
+                gain=1.0, b=1, l=4608, h=24, d=128, q=FAKE, k=FAKE, v=FAKE, ol=4608, oo=0, st=None)
+
+    def call(**kw):
+        a = dict(args, **kw)
+        return f(*a.values())
+
+    assert call(d=64) == _lib.FLK_E_UNSUPPORTED
+    assert call(oo=1) == _lib.FLK_E_INVALID                 # out_offset + L > out_length
+    assert call(rs=9000) == _lib.FLK_E_INVALID              # row shorter than 3*H*D
+    assert call(rs=9220) == _lib.FLK_E_ALIGN                # row stride not a multiple of 8
+    assert call(q=FAKE + 4) == _lib.FLK_E_ALIGN
+    assert call(l=0) == _lib.FLK_OK
+
+
+def test_rope_validation(lib):
+    axes = _lib.int_array([32, 32, 32, 31])
+    assert lib.flk_rope_lanes(FAKE, 4, 10, 4, axes, 2000.0, FAKE, FAKE, None) == _lib.FLK_E_INVALID
+    axes = _lib.int_array([32] * 9)
+    assert lib.flk_rope_embed(FAKE, 9, 10, 9, axes, 2000.0, FAKE, None) == _lib.FLK_E_INVALID
+    assert lib.flk_lane_pair(FAKE + 4, 10, 64, FAKE, FAKE, None) == _lib.FLK_E_ALIGN
+
+
+def test_row_and_score_tiles():
+    assert [kernels.row_tile(n) for n in (4608, 1536, 512, 4096, 16896, 4352, 100)] == \
+        [2304, 1536, 512, 512, 1536, 256, None]
+    assert kernels.row_tile(4608) == P.row_tile(4608)
+
+
+def test_python_errors_follow_the_reference():
+    qkv = torch.zeros(1, 100, 9216, dtype=torch.bfloat16)
+    f = kernels.Freqs(torch.zeros(100, 128), torch.zeros(100, 128))
+    with pytest.raises(ValueError, match="qk_prep needs a row tile dividing L=100"):
+        kernels.qk_prep(qkv, torch.ones(128), torch.ones(128), f, 24)
+    with pytest.raises(ValueError, match="interpret"):
+        kernels.qk_prep(qkv, torch.ones(128), torch.ones(128), f, 24, interpret=True)
+    q = torch.zeros(1, 2, 100, 128, dtype=torch.bfloat16)
+    with pytest.raises(StopIteration):
+        kernels.attend(q, q, q)
+    with pytest.raises(ValueError, match="does not divide"):
+        kernels.attend(q, q, q, block=64)
+    q = torch.zeros(1, 2, 128, 128, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="GPU"):
+        kernels.attend(q, q, q)                              # no CPU fallback
+    with pytest.raises(ValueError, match="GPU"):
+        kernels.qk_prep(torch.zeros(1, 128, 9216, dtype=torch.bfloat16), torch.ones(128), torch.ones(128),
+                        kernels.Freqs(torch.zeros(128, 128), torch.zeros(128, 128)), 24)
+
+
+def test_logit_bound_and_check_match_oracle():
+    rng = np.random.default_rng(0)
+    qs, ks = rng.standard_normal((2, 5, 128)).astype(np.float32)
+    np.testing.assert_allclose(kernels.logit_bound(torch.from_numpy(qs), torch.from_numpy(ks)).numpy(),
+                               P.logit_bound(qs, ks), rtol=1e-6)
+    for v in (1.0, 2.6, 2.7, 3.0):
+        blocks = {"double_blocks": {f"{s}_attn.norm.{n}.scale": np.full((5, 128), v, np.float32)
+                                    for s in ("img", "txt") for n in ("query_norm", "key_norm")},
+                  "single_blocks": {f"norm.{n}.scale": np.ones((20, 128), np.float32)
+                                    for n in ("query_norm", "key_norm")}}
+        try:
+            P.check_logit_bound(blocks)
+            oracle_ok = True
+        except ValueError as e:
+            oracle_ok, msg = False, str(e)
+        if oracle_ok:
+            loader.check_logit_bound(blocks)
+        else:
+            with pytest.raises(ValueError) as info:
+                loader.check_logit_bound(blocks)
+            assert str(info.value) == msg
+    assert loader.sequence_margin(15.6, 4608) > 0 and loader.sequence_margin(80.0, 16896) < 0
+
+
+def test_ids_match_oracle():
+    np.testing.assert_array_equal(rope.img_ids(4, 6), P.img_ids(4, 6))
+    np.testing.assert_array_equal(rope.txt_ids(9), P.txt_ids(9))
+    np.testing.assert_array_equal(rope.sequence_ids(5, 3, 2), P.sequence_ids(5, 3, 2))
+
+
+def test_workload_bookkeeping():
+    w = workloads.WORKLOADS
+    assert [w[n].length for n in ("klein_512", "klein_1024", "klein_1024_b4", "klein_2048", "klein_1536x640")] == \
+        [1536, 4608, 4608, 16896, 4352]
+    assert w["klein_1024"].qk_prep_bytes() == 2 * 4608 * 9216 * 2 + 2 * 4608 * 128 * 4 + 2 * 128 * 2 == 174588416
+    assert w["klein_1024"].attend_flops() == 4 * 24 * 4608 ** 2 * 128 == 260919263232
+    assert math.isclose(workloads.q_gain(w["klein_1024"]), 1 / math.sqrt(128))
+
+
+def test_stress_channels_and_scales():
+    w = workloads.Workload("t", 1, 4, 2, 2, stress_fraction=0.05)
+    plain = workloads.Workload("t", 1, 4, 2, 2)
+    a, b = workloads.make_qkv(w).float(), workloads.make_qkv(plain).float()
+    ratio = (a / torch.where(b == 0, torch.ones_like(b), b))
+    scaled = ((ratio - 8).abs() < 0.1).all(dim=(0, 1))
+    assert int(scaled.sum()) == round(0.05 * 9216)
+    qs, ks = workloads.make_scales(w)
+    assert qs.dtype == torch.bfloat16 and abs(float(qs.float().mean()) - 1) < 0.02
+
+
+def test_cpu_baseline_matches_oracle_plain_path():
+    from oracle import cpu_baseline as cb
+    g = torch.Generator().manual_seed(0)
+    qkv = torch.randn(1, 96, 3 * 2 * 128, generator=g).to(torch.bfloat16)
+    qs = (1 + 0.05 * torch.randn(128, generator=g)).to(torch.bfloat16)
+    ks = (1 + 0.05 * torch.randn(128, generator=g)).to(torch.bfloat16)
+    ids = P.sequence_ids(32, 8, 8)
+    pe = P.embed_nd(ids)
+    got = cb.plain_attention(qkv, qs, ks, torch.from_numpy(pe[0, 0]), 2).numpy()
+    q, k, v = P.qk_prep_plain(qkv.float().numpy(), qs.float().numpy(), ks.float().numpy(), pe, 2)
+    want = P.sdpa(q, k, v)
+    assert np.abs(got - want).max() <= 2e-2 and np.abs(got - want).mean() <= 2e-4
+
+
+def test_bench_refuses_multi_gpu():
+    proc = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"],
+                          capture_output=True, text=True, timeout=120)
+    assert proc.returncode == 2 and "one GPU" in proc.stderr
