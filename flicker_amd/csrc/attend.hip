@@ -29,12 +29,13 @@
 // which keeps every 8 consecutive K rows (b128 operand reads) and every group of 4 V
 // rows x 2 chunks (transpose reads) on distinct banks of the 32-bank LDS.
 //
-// Pipeline.  A 256-thread block (4 waves = one per SIMD, 256 queries) streams tiles
-// through a 3-buffer ring, two 32-key units per tile.  In the phase of unit u the wave
+// Pipeline.  A block of 8 waves (two per SIMD, 32 queries each) streams 64-key tiles,
+// two 32-key units per tile.  In the phase of unit u the wave
 // first issues all 16 LDS operand reads, then alternates each QK^T MFMA of unit u+1
 // with the exp / bf16 / row-sum VALU work of two elements of unit u (explicit schedule
-// fences keep that interleave), then runs the 16 PV MFMAs of unit u.  The copy of tile
-// t+2 is issued in tile t's second phase and waited on before the tile's closing barrier.
+// fences keep that interleave), then runs the 16 PV MFMAs of unit u.  Tiles stream
+// through a 4-buffer ring: the copy of tile t+3 starts with tile t and is waited on two
+// tiles later.
 // Blocks are renumbered so that all query tiles of one head run on the same XCD
 // (hardware deals blocks round-robin over the 8 XCDs), keeping the head's K/V in one L2.
 
@@ -55,7 +56,7 @@ constexpr int kWavesPerSimd = kWaves / 4;
 constexpr int kRowsPerWave = 64 / kWaves;  // tile rows each wave copies
 constexpr int kBM = kWaves * kQB * 32;  // queries per block
 constexpr int kBN = 64;                 // keys per LDS tile (two 32-key units)
-constexpr int kStages = 3;
+constexpr int kStages = 4;
 constexpr int kThreads = kWaves * 64;
 constexpr int kRowBytes = kD * 2;       // one K or V row: 256 B = 16 chunks of 16 B
 constexpr int kTileBytes = kBN * kRowBytes;
@@ -75,7 +76,18 @@ typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 __device__ __forceinline__ int swz(int row) { return ((row & 3) << 1) | ((row >> 2) & 1); }
 
 // Copy one 64-key tile of K and V (rows kv0..kv0+63, clamped to the last row) into `buf`.
-// Each wave moves 64/kWaves rows of K and of V, 4 rows (64 lanes x 16 B) per instruction.
+// Each wave moves 64/kWaves rows of K and of V, 4 rows (64 lanes x 16 B) per instruction:
+// lane i of global_load_lds_dwordx4 lands at M0 + 16 i.  The instruction is issued from
+// inline asm so that the compiler does not order every later LDS read behind it (it cannot
+// prove the ring buffers disjoint); completion is awaited explicitly with vmcnt.
+__device__ __forceinline__ void dma16(const void* src, const uint8_t* lds_dst) {
+  const unsigned m0 = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)lds_dst);
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+               :: "s"(m0), "v"(src) : "memory", "m0");
+}
+
+constexpr int kDmaPerTile = 2 * (kRowsPerWave / 4);  // per wave: K and V instructions of one tile
+
 __device__ __forceinline__ void copy_tile(uint8_t* buf, const uint16_t* __restrict__ kh,
                                           const uint16_t* __restrict__ vh, int kv0, int length,
                                           int wave, int lane) {
@@ -86,9 +98,8 @@ __device__ __forceinline__ void copy_tile(uint8_t* buf, const uint16_t* __restri
     const int chunk = (lane & 15) ^ swz(row);                    // logical chunk for its slot
     const int key = min(kv0 + row, length - 1);
     const int64_t src = (int64_t)key * kD + chunk * 8;
-    const int dst = row0 * kRowBytes;
-    __builtin_amdgcn_global_load_lds(kh + src, (lds_void*)(buf + dst), 16, 0, 0);
-    __builtin_amdgcn_global_load_lds(vh + src, (lds_void*)(buf + kTileBytes + dst), 16, 0, 0);
+    dma16(kh + src, buf + row0 * kRowBytes);
+    dma16(vh + src, buf + kTileBytes + row0 * kRowBytes);
   }
 }
 
@@ -125,18 +136,11 @@ __device__ __forceinline__ uint32_t exp_pair(float s0, float s1, float& lsum, in
 }
 
 // Unit phase: P(u) = exp(S(u)) interleaved with S(u+1) = K(u+1) Q^T, then O^T += V(u)^T P(u)^T.
-struct TileCopy {
-  uint8_t* dst;        // buffer to fill, or nullptr for none
-  const uint16_t* kh;
-  const uint16_t* vh;
-  int kv0, length, wave, lane;
-};
-
 template <bool kMask>
 __device__ __forceinline__ void unit_phase(WaveState& w, const f32x16 (&s_cur)[kQB],
                                            f32x16 (&s_next)[kQB], const uint8_t* k_next,
                                            const uint8_t* v_tile, int ks0, int key_base,
-                                           int length, int g, const TileCopy& copy) {
+                                           int length, int g) {
   bf16x8 kop[8], vop[2][4];
 #pragma unroll
   for (int st = 0; st < 8; ++st) kop[st] = *reinterpret_cast<const bf16x8*>(k_next + w.k_off[st]);
@@ -154,25 +158,50 @@ __device__ __forceinline__ void unit_phase(WaveState& w, const f32x16 (&s_cur)[k
     sv[qb] = s_cur[qb];
     asm volatile("" : "+v"(sv[qb]));
   }
-  // The next tile copy is issued only after this tile's last operand reads: a pending copy
-  // into LDS makes the compiler wait for it before any later LDS read it cannot prove
-  // disjoint, and the only later reads are behind the tile's closing wait anyway.
-  if (copy.dst) copy_tile(copy.dst, copy.kh, copy.vh, copy.kv0, copy.length, copy.wave, copy.lane);
   __builtin_amdgcn_sched_barrier(0);
 
+  // The exp work of the 8*kQB element pairs is software-pipelined across the MFMA slots:
+  // slot n carries the log2(e) multiplies of pair n+2, the exps of pair n+1 and the bf16
+  // pack + row sum of pair n, so no VALU op waits on the one just issued before it.
+  constexpr int kPairs = 8 * kQB;                     // pair n: query block n % kQB, elements 2*(n/kQB), +1
   uint32_t p[kQB][8];
+  float t[kPairs][2], e[kPairs][2];
+  auto stage_mul = [&](int n) {
+    const int qb = n % kQB, i = 2 * (n / kQB);
+    t[n][0] = sv[qb][i] * kLog2e;
+    t[n][1] = sv[qb][i + 1] * kLog2e;
+  };
+  auto stage_exp = [&](int n) {
+    e[n][0] = __builtin_amdgcn_exp2f(t[n][0]);
+    e[n][1] = __builtin_amdgcn_exp2f(t[n][1]);
+  };
+  auto stage_pack = [&](int n) {
+    const int qb = n % kQB, i = 2 * (n / kQB);
+    float e0 = e[n][0], e1 = e[n][1];
+    if constexpr (kMask) {
+      const int key0 = key_base + (i >> 2) * 8 + g * 4 + (i & 3);
+      e0 = key0 < length ? e0 : 0.0f;
+      e1 = key0 + 1 < length ? e1 : 0.0f;
+    }
+    const uint32_t wv = flk::pack_bf16x2(e0, e1);
+    p[qb][i >> 1] = wv;
+    const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
+    w.lsum[qb] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, wv), ones, w.lsum[qb], false);
+  };
 #pragma unroll
   for (int qb = 0; qb < kQB; ++qb) s_next[qb] = f32x16{};
+  stage_mul(0);
+  stage_mul(1);
+  stage_exp(0);
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int st = 0; st < 8; ++st) {
-#pragma unroll
-    for (int qb = 0; qb < kQB; ++qb) {
-      s_next[qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop[st], w.qreg[qb][st], s_next[qb], 0, 0, 0);
-      const int i = 2 * st;  // elements i, i+1 of this query block
-      p[qb][st] = exp_pair<kMask>(sv[qb][i], sv[qb][i + 1], w.lsum[qb],
-                                  key_base + (i >> 2) * 8 + g * 4 + (i & 3), length);
-      __builtin_amdgcn_sched_barrier(0);
-    }
+  for (int n = 0; n < kPairs; ++n) {
+    const int st = n / kQB, qb = n % kQB;              // the MFMA of this slot
+    s_next[qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop[st], w.qreg[qb][st], s_next[qb], 0, 0, 0);
+    if (n + 2 < kPairs) stage_mul(n + 2);
+    if (n + 1 < kPairs) stage_exp(n + 1);
+    stage_pack(n);
+    __builtin_amdgcn_sched_barrier(0);
   }
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
@@ -190,15 +219,13 @@ __device__ __forceinline__ void unit_phase(WaveState& w, const f32x16 (&s_cur)[k
 }
 
 // One 64-key tile = two unit phases.  The second phase computes S of the next tile's first
-// unit (on the last tile it reads a stale buffer; that result is unused) and issues the
-// copy of tile t + 2 into the third buffer.
+// unit (on the last tile it reads a stale buffer; that result is unused).
 template <bool kMask>
 __device__ __forceinline__ void tile_step(WaveState& w, const uint8_t* cur, const uint8_t* nxt,
-                                          int kv0, int length, int g, const TileCopy& copy) {
-  const TileCopy none = {nullptr, nullptr, nullptr, 0, 0, 0, 0};
-  unit_phase<kMask>(w, w.sA, w.sB, cur + kUnitBytes, cur + kTileBytes, 0, kv0, length, g, none);
+                                          int kv0, int length, int g) {
+  unit_phase<kMask>(w, w.sA, w.sB, cur + kUnitBytes, cur + kTileBytes, 0, kv0, length, g);
   __builtin_amdgcn_sched_barrier(0);
-  unit_phase<kMask>(w, w.sB, w.sA, nxt, cur + kTileBytes, 2, kv0 + 32, length, g, copy);
+  unit_phase<kMask>(w, w.sB, w.sA, nxt, cur + kTileBytes, 2, kv0 + 32, length, g);
   __builtin_amdgcn_sched_barrier(0);
 }
 
@@ -244,6 +271,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void attend_kernel(
   const int full_tiles = length / kBN;
   copy_tile(smem, kh, vh, 0, length, wave, lane);
   copy_tile(smem + kBufBytes, kh, vh, kBN, length, wave, lane);
+  copy_tile(smem + 2 * kBufBytes, kh, vh, 2 * kBN, length, wave, lane);
 
   WaveState w;
   const int q0 = qblk * kBM + wave * (kQB * 32);
@@ -275,28 +303,27 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void attend_kernel(
     }
   }
 
-  __builtin_amdgcn_s_waitcnt(0);
+  asm volatile("s_waitcnt vmcnt(%0)" :: "n"(kDmaPerTile) : "memory");  // tiles 0 and 1 landed
   __syncthreads();
   qk_first(w, smem);
 
   // Full tiles, then the partial tail tile (if any) with key masking.  Tile t lives in
-  // buffer t % 3.  The copy of tile t + 2 is unconditional: past the end it re-reads the
-  // last row into the free buffer.
-  int cur = 0;
+  // buffer t % 4.  Iteration t starts the copy of tile t + 3 (into the buffer tile t - 1 has
+  // left) and ends by waiting for all but that copy -- i.e. for tile t + 2, which the next
+  // iteration's second phase reads -- so each copy has two iterations to land.  Copies past
+  // the end re-read the last row into a buffer nobody reads.
   for (int t = 0; t < full_tiles; ++t) {
-    const int nxt = cur == kStages - 1 ? 0 : cur + 1;
-    const int fill = nxt == kStages - 1 ? 0 : nxt + 1;  // buffer of tile t + 2
-    const TileCopy copy = {smem + fill * kBufBytes, kh, vh, (t + 2) * kBN, length, wave, lane};
-    tile_step<false>(w, smem + cur * kBufBytes, smem + nxt * kBufBytes, t * kBN, length, g, copy);
-    __builtin_amdgcn_s_waitcnt(0);
+    copy_tile(smem + ((t + 3) & 3) * kBufBytes, kh, vh, (t + 3) * kBN, length, wave, lane);
+    tile_step<false>(w, smem + (t & 3) * kBufBytes, smem + ((t + 1) & 3) * kBufBytes, t * kBN, length, g);
+    asm volatile("s_waitcnt vmcnt(%0)" :: "n"(kDmaPerTile) : "memory");
     __syncthreads();
-    cur = nxt;
   }
   if (full_tiles < ntiles) {
-    const int nxt = cur == kStages - 1 ? 0 : cur + 1;
-    const TileCopy none = {nullptr, nullptr, nullptr, 0, 0, 0, 0};
-    tile_step<true>(w, smem + cur * kBufBytes, smem + nxt * kBufBytes, full_tiles * kBN, length, g, none);
+    const int t = full_tiles;
+    tile_step<true>(w, smem + (t & 3) * kBufBytes, smem + ((t + 1) & 3) * kBufBytes, t * kBN, length, g);
   }
+  // No copy may still be writing this block's LDS when the block ends.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   // Epilogue: l over both lane halves, O = bf16(acc / l), 4 d values per 8-byte store.
 #pragma unroll
