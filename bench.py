@@ -12,11 +12,18 @@ whose total exceeds it.  A CPU baseline (the torch-CPU restatement of the refere
 plain-XLA path, the oracle) is timed on the host cores.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload klein_1024]
+
+Counter runs (rocprofv3 --pmc) use --only to launch one kernel kind, and
+--ingest-pmc turns a FETCH_SIZE run and a WRITE_SIZE run of
+`--only calibrate` into the per-launch HBM traffic summary
+profiles/hbm_traffic_<workload>.json that the default run reports as roofline.traffic.
 """
 
 from __future__ import annotations
 
 import argparse
+import csv
+import glob
 import json
 import os
 import sys
@@ -26,17 +33,64 @@ HBM_PEAK_GBS = 8000.0           # MI355X HBM3E, GB/s
 BF16_DENSE_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, TFLOP/s
 METRIC = "attend TFLOP/s + qk_prep GB/s at 1024² Klein shape; % of MI355X roofline"
 INFINITY_CACHE_BYTES = 256 * 2 ** 20
+ROOT = os.path.dirname(os.path.abspath(__file__))
+COPY_BYTES = 64 * 2 ** 20       # calibration copy: 64 MiB read + 64 MiB written per launch
 
 
 def parse():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=300,
+                    help="untimed steps; enough (~0.1 s) to bring the GPU to its working clock")
     ap.add_argument("--workload", default="klein_1024")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-reps", type=int, default=3)
+    ap.add_argument("--only", choices=["step", "calibrate"], default="step",
+                    help="calibrate: the step plus a plain device copy of known size, for counter runs")
+    ap.add_argument("--ingest-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="rocprofv3 --pmc output dirs of FETCH_SIZE / WRITE_SIZE runs of --only calibrate")
     return ap.parse_args()
+
+
+def traffic_file(workload: str) -> str:
+    return os.path.join(ROOT, "profiles", f"hbm_traffic_{workload}.json")
+
+
+def _counter_means(directory: str, counter: str) -> dict:
+    files = glob.glob(os.path.join(directory, "**", "*counter_collection.csv"), recursive=True)
+    if not files:
+        raise SystemExit(f"no counter_collection.csv under {directory}")
+    sums: dict = {}
+    for f in files:
+        for row in csv.DictReader(open(f)):
+            if row["Counter_Name"] != counter:
+                continue
+            name = row["Kernel_Name"]
+            key = ("attend" if "attend_kernel" in name else "qk_prep" if "qk_prep_kernel" in name
+                   else "copy" if ("copyBuffer" in name or "copy" in name.lower()) else None)
+            if key:
+                sums.setdefault(key, []).append(float(row["Counter_Value"]))
+    if "copy" in sums:  # keep the calibration copies, not the small host-to-device copies
+        big = max(sums["copy"])
+        sums["copy"] = [v for v in sums["copy"] if v >= 0.5 * big]
+    return {k: sum(v) / len(v) for k, v in sums.items()}
+
+
+def ingest_pmc(fetch_dir: str, write_dir: str, workload: str) -> dict:
+    """Per-launch HBM bytes of each kernel: counter KiB per dispatch scaled by what the same
+    counter reads for the calibration copy (COPY_BYTES read, COPY_BYTES written)."""
+    fetch = _counter_means(fetch_dir, "FETCH_SIZE")
+    write = _counter_means(write_dir, "WRITE_SIZE")
+    f_scale = COPY_BYTES / (fetch["copy"] * 1024)
+    w_scale = COPY_BYTES / (write["copy"] * 1024)
+    out = {"workload": workload, "fetch_scale": f_scale, "write_scale": w_scale,
+           "copy_fetch_kib": fetch["copy"], "copy_write_kib": write["copy"], "kernels": {}}
+    for k in ("qk_prep", "attend"):
+        rb, wb = fetch[k] * 1024 * f_scale, write[k] * 1024 * w_scale
+        out["kernels"][k] = {"fetch_kib": fetch[k], "write_kib": write[k], "read_bytes": rb,
+                             "write_bytes": wb, "traffic_bytes": rb + wb}
+    return out
 
 
 def cpu_baseline(w, qkv, qs, ks, ids, reps: int) -> dict:
@@ -64,6 +118,13 @@ def cpu_baseline(w, qkv, qs, ks, ids, reps: int) -> dict:
 
 def main() -> int:
     args = parse()
+    if args.ingest_pmc:
+        summary = ingest_pmc(args.ingest_pmc[0], args.ingest_pmc[1], args.workload)
+        os.makedirs(os.path.dirname(traffic_file(args.workload)), exist_ok=True)
+        with open(traffic_file(args.workload), "w") as f:
+            json.dump(summary, f, indent=1)
+        print(json.dumps(summary))
+        return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); multi-GPU sharding of this "
               "path is a design note, not a measured configuration", file=sys.stderr)
@@ -86,12 +147,17 @@ def main() -> int:
     set_bytes = 2 * act_bytes + act_bytes // 3
     n_sets = max(2, -(-2 * INFINITY_CACHE_BYTES // set_bytes))
     sets = []
-    for i in range(n_sets):
+    for _ in range(n_sets):
         qkv = qkv_cpu.to(dev)
         out = tuple(torch.empty((w.batch, w.num_heads, w.length, w.head_dim), dtype=torch.bfloat16, device=dev)
                     for _ in range(3))
         o = torch.empty_like(out[0])
         sets.append((qkv, out, o))
+    copies = []
+    if args.only == "calibrate":
+        for _ in range(4):
+            copies.append((torch.empty(COPY_BYTES, dtype=torch.uint8, device=dev).fill_(1),
+                           torch.empty(COPY_BYTES, dtype=torch.uint8, device=dev)))
 
     def step(i, ev=None):
         qkv, out, o = sets[i % n_sets]
@@ -103,6 +169,9 @@ def main() -> int:
         kernels.attend(*out, out=o)
         if ev is not None:
             ev[2].record()
+        if copies:
+            src, dst = copies[i % len(copies)]
+            dst.copy_(src)
 
     for i in range(args.warmup):
         step(i)
@@ -118,6 +187,12 @@ def main() -> int:
     at_ms = sum(e[1].elapsed_time(e[2]) for e in events) / args.steps
     qk_gbs = w.qk_prep_bytes() / (qk_ms * 1e-3) / 1e9
     at_tflops = w.attend_flops() / (at_ms * 1e-3) / 1e12
+
+    traffic = {}
+    if os.path.exists(traffic_file(w.name)):
+        with open(traffic_file(w.name)) as f:
+            traffic = json.load(f)["kernels"]
+    source = os.path.relpath(traffic_file(w.name), ROOT) if traffic else None
 
     result = {
         "metric": METRIC,
@@ -138,14 +213,16 @@ def main() -> int:
                    "buffer_sets": n_sets},
         "roofline": {"bound": "mfma", "achieved": round(at_tflops, 2), "peak": BF16_DENSE_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(at_tflops / BF16_DENSE_PEAK_TFLOPS, 4),
-                     "traffic": None, "kernel": "attend_kernel",
+                     "traffic": round(traffic["attend"]["traffic_bytes"]) if traffic else None,
+                     "traffic_source": source, "kernel": "attend_kernel",
                      "flops_per_launch": w.attend_flops(), "avg_launch_us": round(at_ms * 1e3, 2)},
         "qk_prep": {"roofline": {"bound": "hbm", "achieved": round(qk_gbs, 1), "peak": HBM_PEAK_GBS,
-                                 "unit": "GB/s", "frac": round(qk_gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                                 "kernel": "qk_prep_kernel", "bytes_per_launch": w.qk_prep_bytes(),
-                                 "avg_launch_us": round(qk_ms * 1e3, 2)}},
+                                 "unit": "GB/s", "frac": round(qk_gbs / HBM_PEAK_GBS, 4),
+                                 "traffic": round(traffic["qk_prep"]["traffic_bytes"]) if traffic else None,
+                                 "traffic_source": source, "kernel": "qk_prep_kernel",
+                                 "bytes_per_launch": w.qk_prep_bytes(), "avg_launch_us": round(qk_ms * 1e3, 2)}},
     }
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and args.only == "step":
         result["cpu_baseline"] = cpu_baseline(w, qkv_cpu, qs_cpu, ks_cpu, ids, args.cpu_reps)
     print(json.dumps(result), flush=True)
     return 0
