@@ -26,6 +26,12 @@ SIGNATURES = {
     "flk_rope_embed": (_i, [_p, _i64, _i64, _i, _ip, _f, _p, _p]),
     "flk_lane_pair": (_i, [_p, _i64, _i, _p, _p, _p]),
     "flk_rope_lanes": (_i, [_p, _i64, _i64, _i, _ip, _f, _p, _p, _p]),
+    "flk_absmax_rows": (_i, [_p, _i64, _i64, _i64, _p, _p]),
+    "flk_absmax_cols": (_i, [_p, _i64, _i64, _i64, _i, _p, _p]),
+    "flk_smooth_factors": (_i, [_p, _p, _i64, _p, _p, _p]),
+    "flk_quantize_weight": (_i, [_p, _i64, _p, _i, _i, _p, _p, _p]),
+    "flk_quantize_act": (_i, [_p, _i64, _p, _i, _i, _p, _p, _p]),
+    "flk_w8a8_gemm": (_i, [_p, _p, _p, _p, _i, _i, _i, _p, _i64, _p, _p]),
 }
 
 ABI_VERSION = 1

@@ -80,12 +80,6 @@ __device__ __forceinline__ int swz(int row) { return ((row & 3) << 1) | ((row >>
 // lane i of global_load_lds_dwordx4 lands at M0 + 16 i.  The instruction is issued from
 // inline asm so that the compiler does not order every later LDS read behind it (it cannot
 // prove the ring buffers disjoint); completion is awaited explicitly with vmcnt.
-__device__ __forceinline__ void dma16(const void* src, const uint8_t* lds_dst) {
-  const unsigned m0 = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)lds_dst);
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
-               :: "s"(m0), "v"(src) : "memory", "m0");
-}
-
 constexpr int kDmaPerTile = 2 * (kRowsPerWave / 4);  // per wave: K and V instructions of one tile
 
 __device__ __forceinline__ void copy_tile(uint8_t* buf, const uint16_t* __restrict__ kh,
@@ -98,8 +92,8 @@ __device__ __forceinline__ void copy_tile(uint8_t* buf, const uint16_t* __restri
     const int chunk = (lane & 15) ^ swz(row);                    // logical chunk for its slot
     const int key = min(kv0 + row, length - 1);
     const int64_t src = (int64_t)key * kD + chunk * 8;
-    dma16(kh + src, buf + row0 * kRowBytes);
-    dma16(vh + src, buf + kTileBytes + row0 * kRowBytes);
+    flk::dma16(kh + src, buf + row0 * kRowBytes);
+    flk::dma16(vh + src, buf + kTileBytes + row0 * kRowBytes);
   }
 }
 

@@ -1,0 +1,576 @@
+// w8a8: SmoothQuant int8 QKV projection for gfx950 (int8 MFMA, int32 accumulate).
+//
+// The reference projects x @ w in bf16 (src/flicker/nn.py:13-14, called for the QKV
+// projection at src/flicker/modules.py:128,132,186) and has no quantisation.  This file
+// implements the replacement defined by the formula below; every integer and every
+// float32 rounding is reproduced exactly (each float op is one IEEE f32 operation with
+// round-to-nearest-even; division and sqrt correctly rounded; rint ties-to-even):
+//
+//   calibration   s_j = sqrt(max_t |X[t,j]|) / sqrt(max_o |W[j,o]|)  (1 if either is 0)
+//                 inv_s_j = 1 / s_j
+//   weight        Wh[j,o] = f32(W[j,o]) * s_j;  w_o = max_j |Wh[j,o]| / 127 (1 if 0)
+//                 Wq[j,o] = clamp(rint(Wh[j,o] / w_o), -127, 127)           int8
+//   activation    Xh[t,j] = f32(X[t,j]) * inv_s_j;  a_t = max_j |Xh[t,j]| / 127 (1 if 0)
+//                 Xq[t,j] = clamp(rint(Xh[t,j] / a_t), -127, 127)           int8
+//   GEMM          acc[t,o] = sum_j Xq[t,j] * Wq[j,o]                          int32, exact
+//   rescale       Y[t,o] = bf16((f32(acc[t,o]) * a_t) * w_o)
+//
+// Layouts: X (M, K) and W (K, N) bf16 row-major with row strides (W as the reference
+// stores it: in x out); Xq (M, K) int8; the quantised weight is stored transposed,
+// WqT (N, K) int8, so both GEMM operands are K-contiguous rows; Y (M, N) bf16 with a
+// row stride; optional acc (M, N) int32.
+//
+// GEMM.  A block of 4 waves owns a 256 (n) x 256 (m) output tile and computes it
+// transposed, Y^T = WqT . Xq^T, with v_mfma_i32_32x32x32_i8: A operand = 32 WqT rows x
+// 32 k bytes, B operand = 32 Xq rows x 32 k bytes, both one ds_read_b128 per lane.  In
+// the 32x32 accumulator a lane owns one token and 4 x 4 consecutive output channels, so
+// the epilogue stores 4 bf16 (8 bytes) per register group.  Each wave holds a 128 x 128
+// sub-tile: 16 accumulators of 16 int32 (256 registers), 8 operand reads per 16 MFMAs.
+// k advances in 64-byte stages through a 4-stage LDS ring filled by
+// global_load_lds_dwordx4 (no registers); stage rows are 64 bytes = 4 chunks of 16 B
+// stored at chunk ^ ((row >> 1) & 3), which keeps each 8-lane phase of an operand read
+// on distinct banks.  Blocks are renumbered so consecutive output tiles share an XCD
+// (and its L2), and grouped so that 4 token tiles sweep the channel tiles together.
+
+#include "common.h"
+
+namespace {
+
+using flk::f32x4;
+using flk::i32x4;
+using flk::i32x16;
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr float kQMax = 127.0f;
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) v = fmaxf(v, __shfl_xor(v, d));
+  return v;
+}
+
+__device__ __forceinline__ float absmax_scale(float amax) { return amax > 0.0f ? amax / kQMax : 1.0f; }
+
+// clamp(rint(v / scale), -127, 127) as an integer.
+__device__ __forceinline__ int quantize(float v, float scale) {
+  const float q = __builtin_rintf(v / scale);
+  return (int)fminf(fmaxf(q, -kQMax), kQMax);
+}
+
+__device__ __forceinline__ uint32_t pack_i8x4(int a, int b, int c, int d) {
+  return (uint32_t)(a & 0xFF) | ((uint32_t)(b & 0xFF) << 8) | ((uint32_t)(c & 0xFF) << 16) |
+         ((uint32_t)(d & 0xFF) << 24);
+}
+
+__device__ __forceinline__ void unpack_bf16x8(const uint4& r, float (&f)[8]) {
+  f[0] = flk::bf16_lo(r.x); f[1] = flk::bf16_hi(r.x);
+  f[2] = flk::bf16_lo(r.y); f[3] = flk::bf16_hi(r.y);
+  f[4] = flk::bf16_lo(r.z); f[5] = flk::bf16_hi(r.z);
+  f[6] = flk::bf16_lo(r.w); f[7] = flk::bf16_hi(r.w);
+}
+
+// ---------------------------------------------------------------- calibration ----------
+
+// out[r] = max_c |x[r, c]|; one wave per row, 8 columns per lane step (cols % 8 == 0).
+__global__ __launch_bounds__(256) void absmax_rows_kernel(const uint16_t* __restrict__ x, int64_t rows,
+                                                          int64_t cols, int64_t stride,
+                                                          float* __restrict__ out) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + wave;
+  if (row >= rows) return;
+  const uint16_t* p = x + row * stride;
+  float m = 0.0f;
+  for (int64_t c = (int64_t)lane * 8; c < cols; c += 512) {
+    float f[8];
+    unpack_bf16x8(*reinterpret_cast<const uint4*>(p + c), f);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(f[i]));
+  }
+  m = wave_max(m);
+  if (lane == 0) out[row] = m;
+}
+
+// out[c] = max_r |x[r, c]| (or max with the existing out[c] when accumulating over
+// calibration batches).  A block covers 128 columns: 16 lane groups of 8 columns x 16 row
+// groups, reduced through LDS; each column has exactly one writer.
+__global__ __launch_bounds__(256) void absmax_cols_kernel(const uint16_t* __restrict__ x, int64_t rows,
+                                                          int64_t cols, int64_t stride, int accumulate,
+                                                          float* __restrict__ out) {
+  __shared__ float red[16][129];
+  const int cg = threadIdx.x & 15, rg = threadIdx.x >> 4;
+  const int64_t c0 = (int64_t)blockIdx.x * 128 + cg * 8;
+  float m[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  if (c0 < cols) {
+    for (int64_t r = rg; r < rows; r += 16) {
+      float f[8];
+      unpack_bf16x8(*reinterpret_cast<const uint4*>(x + r * stride + c0), f);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) m[i] = fmaxf(m[i], fabsf(f[i]));
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) red[rg][cg * 8 + i] = m[i];
+  __syncthreads();
+  if (threadIdx.x < 128) {
+    const int64_t c = (int64_t)blockIdx.x * 128 + threadIdx.x;
+    if (c < cols) {
+      float v = 0.0f;
+#pragma unroll
+      for (int g = 0; g < 16; ++g) v = fmaxf(v, red[g][threadIdx.x]);
+      if (accumulate) v = fmaxf(v, out[c]);
+      out[c] = v;
+    }
+  }
+}
+
+// s = sqrt(xa) / sqrt(wa) (1 where either maximum is 0), inv_s = 1 / s.
+__global__ void smooth_factors_kernel(const float* __restrict__ xa, const float* __restrict__ wa, int64_t k,
+                                      float* __restrict__ s, float* __restrict__ inv_s) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= k) return;
+  const float a = xa[i], b = wa[i];
+  const float v = (a > 0.0f && b > 0.0f) ? __builtin_sqrtf(a) / __builtin_sqrtf(b) : 1.0f;
+  s[i] = v;
+  inv_s[i] = 1.0f / v;
+}
+
+// ---------------------------------------------------------------- quantisation ---------
+
+// Weight (offline): one block per 64 output channels.  Pass 1: column absmax of Wh over all
+// K (8 channel groups x 32 row groups, LDS reduction) -> w_scale.  Pass 2: 64-row k tiles
+// are quantised into an LDS tile [channel][k] and written as 64-byte runs of WqT rows.
+__global__ __launch_bounds__(256) void quantize_weight_kernel(const uint16_t* __restrict__ w, int64_t w_stride,
+                                                              const float* __restrict__ s, int K, int N,
+                                                              int8_t* __restrict__ wqt,
+                                                              float* __restrict__ w_scale) {
+  __shared__ float red[32][65];
+  __shared__ float scale[64];
+  __shared__ __attribute__((aligned(16))) uint8_t tile[64][80];
+  const int tid = threadIdx.x;
+  const int cg = tid & 7, rg = tid >> 3;
+  const int n0 = blockIdx.x * 64;
+  const int nc = n0 + cg * 8;
+  const bool active = nc < N;
+
+  float m[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  if (active) {
+    for (int j = rg; j < K; j += 32) {
+      const float sj = s[j];
+      float f[8];
+      unpack_bf16x8(*reinterpret_cast<const uint4*>(w + (int64_t)j * w_stride + nc), f);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) m[i] = fmaxf(m[i], fabsf(f[i] * sj));
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) red[rg][cg * 8 + i] = m[i];
+  __syncthreads();
+  if (tid < 64) {
+    float v = 0.0f;
+#pragma unroll 8
+    for (int g = 0; g < 32; ++g) v = fmaxf(v, red[g][tid]);
+    const float sc = absmax_scale(v);
+    scale[tid] = sc;
+    if (n0 + tid < N) w_scale[n0 + tid] = sc;
+  }
+  __syncthreads();
+
+  float sc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) sc[i] = scale[cg * 8 + i];
+  for (int k0 = 0; k0 < K; k0 += 64) {
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+      const int r = rg + it * 32;
+      const int j = k0 + r;
+      if (active) {
+        const float sj = s[j];
+        float f[8];
+        unpack_bf16x8(*reinterpret_cast<const uint4*>(w + (int64_t)j * w_stride + nc), f);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) tile[cg * 8 + i][r] = (uint8_t)quantize(f[i] * sj, sc[i]);
+      }
+    }
+    __syncthreads();
+    const int n = tid >> 2, ch = tid & 3;
+    if (n0 + n < N)
+      *reinterpret_cast<uint4*>(wqt + (int64_t)(n0 + n) * K + k0 + ch * 16) =
+          *reinterpret_cast<const uint4*>(&tile[n][ch * 16]);
+    __syncthreads();
+  }
+}
+
+// Activation (per forward): one wave per token row, the row held in registers
+// (kChunks x 8 elements per lane), absmax reduced across the wave.
+template <int kChunks>
+__global__ __launch_bounds__(256) void quantize_act_kernel(const uint16_t* __restrict__ x, int64_t x_stride,
+                                                           const float* __restrict__ inv_s, int M, int K,
+                                                           int8_t* __restrict__ xq,
+                                                           float* __restrict__ a_scale) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + wave;
+  if (row >= M) return;
+  const int nch = K >> 3;
+  const uint16_t* src = x + (int64_t)row * x_stride;
+  uint4 raw[kChunks];
+#pragma unroll
+  for (int c = 0; c < kChunks; ++c) {
+    const int idx = c * 64 + lane;
+    u32x4 v = {0, 0, 0, 0};
+    if (idx < nch) v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src) + idx);
+    raw[c] = uint4{v.x, v.y, v.z, v.w};
+  }
+  float xh[kChunks][8];
+  float amax = 0.0f;
+#pragma unroll
+  for (int c = 0; c < kChunks; ++c) {
+    const int idx = c * 64 + lane;
+    const f32x4 s0 = idx < nch ? reinterpret_cast<const f32x4*>(inv_s)[2 * idx] : f32x4{0, 0, 0, 0};
+    const f32x4 s1 = idx < nch ? reinterpret_cast<const f32x4*>(inv_s)[2 * idx + 1] : f32x4{0, 0, 0, 0};
+    float f[8];
+    unpack_bf16x8(raw[c], f);
+    const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      xh[c][i] = f[i] * sv[i];
+      amax = fmaxf(amax, fabsf(xh[c][i]));
+    }
+  }
+  const float a = absmax_scale(wave_max(amax));
+  int8_t* dst = xq + (int64_t)row * K;
+#pragma unroll
+  for (int c = 0; c < kChunks; ++c) {
+    const int idx = c * 64 + lane;
+    if (idx < nch) {
+      uint2 packed;
+      packed.x = pack_i8x4(quantize(xh[c][0], a), quantize(xh[c][1], a), quantize(xh[c][2], a), quantize(xh[c][3], a));
+      packed.y = pack_i8x4(quantize(xh[c][4], a), quantize(xh[c][5], a), quantize(xh[c][6], a), quantize(xh[c][7], a));
+      reinterpret_cast<uint2*>(dst)[idx] = packed;
+    }
+  }
+  if (lane == 0) a_scale[row] = a;
+}
+
+// ---------------------------------------------------------------- GEMM -----------------
+
+constexpr int kGT = 256;                 // tile edge: tokens and output channels
+constexpr int kGK = 128;                 // k bytes per stage: one full 128-byte line per row
+constexpr int kGHalf = kGT * kGK;        // one operand's stage: 32 KiB
+constexpr int kGStage = 2 * kGHalf;      // WqT rows, then Xq rows; two stages fill 128 KiB
+constexpr int kGThreads = 256;
+constexpr int kGCopies = 8;              // copy instructions per operand per wave and stage
+#ifndef FLK_GEMM_GROUP
+#define FLK_GEMM_GROUP 4
+#endif
+constexpr int kGroup = FLK_GEMM_GROUP;   // token tiles that sweep the channel tiles together
+constexpr int kXcds = 8;
+
+// LDS slot of 16-byte chunk c in row r is c ^ gswz(r).  An operand read takes chunk
+// 2 ks + half of rows r0 .. r0+31 (one row per lane): every 8 consecutive rows land on 8
+// distinct 16-byte slots of a 128-byte bank line, and every 16 consecutive rows on 16
+// distinct (row parity, slot) pairs, so neither 8-lane nor 16-lane read phases collide.
+__device__ __forceinline__ int gswz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
+
+// One 32-byte k step of the wave's 128 x 128 sub-tile: 16 MFMAs on the fragments in `cur`,
+// interleaved with the reads of the next step's fragments into `nxt` and, in the step that
+// follows the barrier, the copies that refill the stage just consumed.
+template <bool kCopy>
+__device__ __forceinline__ void gemm_step(i32x16 (&acc)[4][4], const i32x4 (&cur)[8], i32x4 (&nxt)[8],
+                                          const uint8_t* src, int off, int wn, int wm, const int8_t* abase,
+                                          const int8_t* bbase, const uint32_t (&aoff)[kGCopies],
+                                          const uint32_t (&boff)[kGCopies], uint8_t* dst) {
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int i = 2 * nt + j;
+      const uint8_t* base = i < 4 ? src + (wn * 128 + i * 32) * kGK : src + kGHalf + (wm * 128 + (i - 4) * 32) * kGK;
+      nxt[i] = *reinterpret_cast<const i32x4*>(base + off);
+      if constexpr (kCopy) {
+        flk::dma16_at(abase, aoff[i], dst + i * 8 * kGK);
+        flk::dma16_at(bbase, boff[i], dst + kGHalf + i * 8 * kGK);
+      }
+    }
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+      acc[nt][mt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(cur[nt], cur[4 + mt], acc[nt][mt], 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// kAcc: also write the exact int32 products (a test and debugging path; its accumulator
+// copies cost registers, so the production instantiation leaves it out).
+template <bool kAcc>
+__global__ __launch_bounds__(kGThreads, 1) void w8a8_gemm_kernel(
+    const int8_t* __restrict__ xq, const int8_t* __restrict__ wqt, const float* __restrict__ a_scale,
+    const float* __restrict__ w_scale, uint16_t* __restrict__ y, int64_t y_stride,
+    int32_t* __restrict__ acc_out, int M, int K, int N, int tiles_m, int tiles_n) {
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * kGStage];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+
+  // Tile order: blocks are dealt round-robin over the XCDs; renumber so that each XCD runs
+  // a contiguous range of logical tiles, then walk kGroup token tiles across all channel
+  // tiles before moving on.
+  const int nblocks = gridDim.x;
+  const int xcd = blockIdx.x % kXcds, local = blockIdx.x / kXcds;
+  const int per = nblocks / kXcds, extra = nblocks % kXcds;
+  const int logical = xcd * per + min(xcd, extra) + local;
+  const int group_tiles = kGroup * tiles_n;
+  const int group = logical / group_tiles;
+  const int first_m = group * kGroup;
+  const int gm = min(kGroup, tiles_m - first_m);
+  const int in_group = logical - group * group_tiles;
+  const int m0 = (first_m + in_group % gm) * kGT;
+  const int n0 = (in_group / gm) * kGT;
+
+  // Copy sources: this wave fills rows wave*64 .. +63 of both operands, 8 rows (64 lanes x
+  // 16 B) per instruction; lane i lands at row i/8, slot i%8, and fetches chunk slot^gswz.
+  // Rows past the matrix edge repeat the last row (their results are never stored).  The
+  // tile's first row (plus the stage's k offset) is a scalar base; lanes add 32-bit offsets.
+  const int8_t* abase = wqt + (int64_t)n0 * K;
+  const int8_t* bbase = xq + (int64_t)m0 * K;
+  uint32_t aoff[kGCopies], boff[kGCopies];
+#pragma unroll
+  for (int i = 0; i < kGCopies; ++i) {
+    const int row = wave * 64 + i * 8 + (lane >> 3);
+    const uint32_t chunk = (uint32_t)(((lane & 7) ^ gswz(row)) * 16);
+    aoff[i] = (uint32_t)min(row, N - 1 - n0) * (uint32_t)K + chunk;
+    boff[i] = (uint32_t)min(row, M - 1 - m0) * (uint32_t)K + chunk;
+  }
+  uint8_t* const wave_lds = smem + wave * 64 * kGK;   // this wave's copy rows in stage 0
+
+  const int KT = K / kGK;
+  const int wn = wave >> 1, wm = wave & 1;
+  const int l32 = lane & 31, half = lane >> 5;
+  int off[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) off[ks] = l32 * kGK + (((2 * ks + half) ^ gswz(l32)) * 16);
+
+  // The epilogue's scales, fetched now so their latency hides behind the main loop: a_t of
+  // the lane's 4 tokens and w_o of its 4 x 4 groups of 4 channels (clamped at the edges;
+  // clamped values are never stored).
+  float am[4];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) am[mt] = a_scale[min(m0 + wm * 128 + mt * 32 + l32, M - 1)];
+  f32x4 ws[4][4];
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+      ws[nt][g] = *reinterpret_cast<const f32x4*>(w_scale + min(n0 + wn * 128 + nt * 32 + g * 8 + half * 4, N - 4));
+
+  i32x16 acc[4][4];
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int b = 0; b < 4; ++b) acc[a][b] = i32x16{};
+
+  // Two stages.  Iteration kt multiplies k steps 0..2 of stage kt while reading the next
+  // step's fragments; then, once stage kt+1 has landed everywhere and every wave has read
+  // all of stage kt (the barrier), step 3 refills stage kt's buffer with stage kt+2 and
+  // reads step 0 of stage kt+1.  Past the last stage the copies repeat it (into the buffer
+  // no later step reads), so every iteration issues the same copies and vmcnt(0) is exact.
+  const int k1 = min(1, KT - 1) * kGK;
+#pragma unroll
+  for (int i = 0; i < kGCopies; ++i) {
+    flk::dma16_at(abase, aoff[i], wave_lds + i * 8 * kGK);
+    flk::dma16_at(bbase, boff[i], wave_lds + kGHalf + i * 8 * kGK);
+  }
+#pragma unroll
+  for (int i = 0; i < kGCopies; ++i) {
+    flk::dma16_at(abase + k1, aoff[i], wave_lds + kGStage + i * 8 * kGK);
+    flk::dma16_at(bbase + k1, boff[i], wave_lds + kGStage + kGHalf + i * 8 * kGK);
+  }
+  asm volatile("s_waitcnt vmcnt(%0)" :: "n"(2 * kGCopies) : "memory");   // stage 0 landed
+  __syncthreads();
+  i32x4 ra[8], rb[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint8_t* base = i < 4 ? smem + (wn * 128 + i * 32) * kGK : smem + kGHalf + (wm * 128 + (i - 4) * 32) * kGK;
+    ra[i] = *reinterpret_cast<const i32x4*>(base + off[0]);
+  }
+
+  for (int kt = 0; kt < KT; ++kt) {
+    const int cur = (kt & 1) * kGStage, nxt = ((kt + 1) & 1) * kGStage;
+    const int k_next = min(kt + 2, KT - 1) * kGK;
+    gemm_step<false>(acc, ra, rb, smem + cur, off[1], wn, wm, abase, bbase, aoff, boff, nullptr);
+    gemm_step<false>(acc, rb, ra, smem + cur, off[2], wn, wm, abase, bbase, aoff, boff, nullptr);
+    gemm_step<false>(acc, ra, rb, smem + cur, off[3], wn, wm, abase, bbase, aoff, boff, nullptr);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // stage kt+1 landed
+    __syncthreads();
+    gemm_step<true>(acc, rb, ra, smem + nxt, off[0], wn, wm, abase + k_next, bbase + k_next, aoff, boff,
+                    wave_lds + cur);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  if constexpr (kAcc) {
+    // Exact int32 products, straight from the accumulators.
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int n = n0 + wn * 128 + nt * 32 + g * 8 + half * 4;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+          const int m = m0 + wm * 128 + mt * 32 + l32;
+          if (n < N && m < M)
+            *reinterpret_cast<i32x4*>(acc_out + (int64_t)m * N + n) =
+                i32x4{acc[nt][mt][4 * g], acc[nt][mt][4 * g + 1], acc[nt][mt][4 * g + 2], acc[nt][mt][4 * g + 3]};
+        }
+      }
+  }
+
+  // Epilogue.  The lane owns token m = mt*32 + l32 and, per register group g, channels
+  // n = nt*32 + 8g + 4*half .. +3 of the wave's 128 x 128 sub-tile.  Rescaled bf16 values go
+  // to this wave's 32 KiB of the (now idle) LDS as [m][n] rows of 256 B whose 16-byte chunks
+  // are XOR-swizzled by m & 15; then the wave reads back 4 rows per instruction (16 lanes x
+  // 16 B per row) and writes each row's 256 contiguous bytes with 16-byte stores.
+  __syncthreads();   // every wave is done reading the operand stages
+  uint8_t* const out_lds = smem + wave * (128 * 256);
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) {
+        const int ml = mt * 32 + l32;
+        const f32x4 w4 = ws[nt][g];
+        const float y0 = ((float)acc[nt][mt][4 * g + 0] * am[mt]) * w4.x;
+        const float y1 = ((float)acc[nt][mt][4 * g + 1] * am[mt]) * w4.y;
+        const float y2 = ((float)acc[nt][mt][4 * g + 2] * am[mt]) * w4.z;
+        const float y3 = ((float)acc[nt][mt][4 * g + 3] * am[mt]) * w4.w;
+        uint2 packed;
+        packed.x = flk::pack_bf16x2(y0, y1);
+        packed.y = flk::pack_bf16x2(y2, y3);
+        const int chunk = (nt * 4 + g) ^ (ml & 15);
+        *reinterpret_cast<uint2*>(out_lds + ml * 256 + chunk * 16 + half * 8) = packed;
+      }
+    }
+  }
+  // Each wave reads back only what it wrote itself: its LDS writes complete in order before
+  // its reads (the compiler waits on lgkmcnt), so no barrier is needed here.
+  const int n_lane = n0 + wn * 128 + (lane & 15) * 8;
+  const bool wide = (y_stride & 7) == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0;   // 16-byte rows
+#pragma unroll 8
+  for (int it = 0; it < 32; ++it) {
+    const int ml = it * 4 + (lane >> 4);
+    const uint4 v = *reinterpret_cast<const uint4*>(out_lds + ml * 256 + (((lane & 15) ^ (ml & 15)) * 16));
+    const int m = m0 + wm * 128 + ml;
+    if (m < M && n_lane < N) {
+      uint16_t* dst = y + (int64_t)m * y_stride + n_lane;
+      if (wide && n_lane + 8 <= N) {
+        *reinterpret_cast<uint4*>(dst) = v;
+      } else {
+        *reinterpret_cast<uint2*>(dst) = uint2{v.x, v.y};
+        if (n_lane + 8 <= N) *reinterpret_cast<uint2*>(dst + 4) = uint2{v.z, v.w};
+      }
+    }
+  }
+}
+
+inline hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
+
+}  // namespace
+
+extern "C" int flk_absmax_rows(const void* x, int64_t rows, int64_t cols, int64_t row_stride, float* out,
+                               void* stream) {
+  if (rows < 0 || cols < 0 || row_stride < cols) return FLK_E_INVALID;
+  if (rows == 0) return FLK_OK;
+  if (!x || !out || cols == 0) return FLK_E_INVALID;
+  if (cols % 8 || row_stride % 8 || !flk_host_aligned(x, 16) || !flk_host_aligned(out, 4)) return FLK_E_ALIGN;
+  const int64_t blocks = (rows + 3) / 4;
+  if (blocks > INT32_MAX) return FLK_E_INVALID;
+  hipLaunchKernelGGL(absmax_rows_kernel, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream),
+                     static_cast<const uint16_t*>(x), rows, cols, row_stride, out);
+  return flk_launch_status();
+}
+
+extern "C" int flk_absmax_cols(const void* x, int64_t rows, int64_t cols, int64_t row_stride, int accumulate,
+                               float* out, void* stream) {
+  if (rows < 0 || cols < 0 || row_stride < cols) return FLK_E_INVALID;
+  if (cols == 0 || (rows == 0 && accumulate)) return FLK_OK;
+  if (!out || (rows > 0 && !x)) return FLK_E_INVALID;
+  if (cols % 8 || row_stride % 8 || (x && !flk_host_aligned(x, 16)) || !flk_host_aligned(out, 4))
+    return FLK_E_ALIGN;
+  const int64_t blocks = (cols + 127) / 128;
+  if (blocks > INT32_MAX) return FLK_E_INVALID;
+  hipLaunchKernelGGL(absmax_cols_kernel, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream),
+                     static_cast<const uint16_t*>(x), rows, cols, row_stride, accumulate, out);
+  return flk_launch_status();
+}
+
+extern "C" int flk_smooth_factors(const float* x_absmax, const float* w_absmax, int64_t k, float* s,
+                                  float* inv_s, void* stream) {
+  if (k < 0) return FLK_E_INVALID;
+  if (k == 0) return FLK_OK;
+  if (!x_absmax || !w_absmax || !s || !inv_s) return FLK_E_INVALID;
+  const int64_t blocks = (k + 255) / 256;
+  if (blocks > INT32_MAX) return FLK_E_INVALID;
+  hipLaunchKernelGGL(smooth_factors_kernel, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream), x_absmax,
+                     w_absmax, k, s, inv_s);
+  return flk_launch_status();
+}
+
+extern "C" int flk_quantize_weight(const void* w, int64_t w_row_stride, const float* s, int k, int n,
+                                   int8_t* wq_t, float* w_scale, void* stream) {
+  if (k < 0 || n < 0 || w_row_stride < n) return FLK_E_INVALID;
+  if (k == 0 || n == 0) return FLK_OK;
+  if (!w || !s || !wq_t || !w_scale) return FLK_E_INVALID;
+  if (k % 64 || n % 8 || w_row_stride % 8) return FLK_E_UNSUPPORTED;
+  if (!flk_host_aligned(w, 16) || !flk_host_aligned(wq_t, 16) || !flk_host_aligned(s, 4) ||
+      !flk_host_aligned(w_scale, 4))
+    return FLK_E_ALIGN;
+  hipLaunchKernelGGL(quantize_weight_kernel, dim3((unsigned)((n + 63) / 64)), dim3(256), 0, as_stream(stream),
+                     static_cast<const uint16_t*>(w), w_row_stride, s, k, n, wq_t, w_scale);
+  return flk_launch_status();
+}
+
+extern "C" int flk_quantize_act(const void* x, int64_t x_row_stride, const float* inv_s, int m, int k,
+                                int8_t* xq, float* a_scale, void* stream) {
+  if (m < 0 || k < 0 || x_row_stride < k) return FLK_E_INVALID;
+  if (m == 0 || k == 0) return FLK_OK;
+  if (!x || !inv_s || !xq || !a_scale) return FLK_E_INVALID;
+  if (k % 8 || k > 8192) return FLK_E_UNSUPPORTED;
+  if (x_row_stride % 8 || !flk_host_aligned(x, 16) || !flk_host_aligned(inv_s, 16) || !flk_host_aligned(xq, 8) ||
+      !flk_host_aligned(a_scale, 4))
+    return FLK_E_ALIGN;
+  const int chunks = (k / 8 + 63) / 64;
+  const dim3 grid((unsigned)((m + 3) / 4)), block(256);
+  const hipStream_t st = as_stream(stream);
+  const uint16_t* xs = static_cast<const uint16_t*>(x);
+  if (chunks <= 1)       hipLaunchKernelGGL(quantize_act_kernel<1>, grid, block, 0, st, xs, x_row_stride, inv_s, m, k, xq, a_scale);
+  else if (chunks <= 2)  hipLaunchKernelGGL(quantize_act_kernel<2>, grid, block, 0, st, xs, x_row_stride, inv_s, m, k, xq, a_scale);
+  else if (chunks <= 4)  hipLaunchKernelGGL(quantize_act_kernel<4>, grid, block, 0, st, xs, x_row_stride, inv_s, m, k, xq, a_scale);
+  else if (chunks <= 6)  hipLaunchKernelGGL(quantize_act_kernel<6>, grid, block, 0, st, xs, x_row_stride, inv_s, m, k, xq, a_scale);
+  else if (chunks <= 8)  hipLaunchKernelGGL(quantize_act_kernel<8>, grid, block, 0, st, xs, x_row_stride, inv_s, m, k, xq, a_scale);
+  else if (chunks <= 12) hipLaunchKernelGGL(quantize_act_kernel<12>, grid, block, 0, st, xs, x_row_stride, inv_s, m, k, xq, a_scale);
+  else                   hipLaunchKernelGGL(quantize_act_kernel<16>, grid, block, 0, st, xs, x_row_stride, inv_s, m, k, xq, a_scale);
+  return flk_launch_status();
+}
+
+extern "C" int flk_w8a8_gemm(const int8_t* xq, const int8_t* wq_t, const float* a_scale, const float* w_scale,
+                             int m, int k, int n, void* y, int64_t y_row_stride, int32_t* acc_or_null,
+                             void* stream) {
+  if (m < 0 || k < 0 || n < 0 || y_row_stride < n) return FLK_E_INVALID;
+  if (m == 0 || n == 0) return FLK_OK;
+  if (!xq || !wq_t || !a_scale || !w_scale || !y || k == 0) return FLK_E_INVALID;
+  if (k % 128 || n % 4) return FLK_E_UNSUPPORTED;
+  if ((int64_t)k * 127 * 127 > INT32_MAX) return FLK_E_UNSUPPORTED;   // int32 accumulation must be exact
+  if (!flk_host_aligned(xq, 16) || !flk_host_aligned(wq_t, 16) || !flk_host_aligned(w_scale, 16) ||
+      !flk_host_aligned(a_scale, 4) || !flk_host_aligned(y, 8) || y_row_stride % 4 ||
+      (acc_or_null && !flk_host_aligned(acc_or_null, 16)))
+    return FLK_E_ALIGN;
+  const int tiles_m = (m + kGT - 1) / kGT, tiles_n = (n + kGT - 1) / kGT;
+  const int64_t blocks = (int64_t)tiles_m * tiles_n;
+  if (blocks > INT32_MAX) return FLK_E_INVALID;
+  if (acc_or_null)
+    hipLaunchKernelGGL(w8a8_gemm_kernel<true>, dim3((unsigned)blocks), dim3(kGThreads), 0, as_stream(stream), xq,
+                       wq_t, a_scale, w_scale, static_cast<uint16_t*>(y), y_row_stride, acc_or_null, m, k, n, tiles_m,
+                       tiles_n);
+  else
+    hipLaunchKernelGGL(w8a8_gemm_kernel<false>, dim3((unsigned)blocks), dim3(kGThreads), 0, as_stream(stream), xq,
+                       wq_t, a_scale, w_scale, static_cast<uint16_t*>(y), y_row_stride, nullptr, m, k, n, tiles_m,
+                       tiles_n);
+  return flk_launch_status();
+}

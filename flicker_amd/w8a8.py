@@ -1,0 +1,168 @@
+"""SmoothQuant W8A8 replacement of the bf16 QKV projection.
+
+The reference projects with ``linear(x, w) = x @ w`` in bf16 (src/flicker/nn.py:13-14)
+at the QKV projections of src/flicker/modules.py:128,132 (double blocks, img/txt) and
+:186 (single blocks, the qkv part of linear1).  It has no quantisation; this module
+defines the int8 replacement by an explicit formula (reproduced bit for bit by the HIP
+kernels of libflicker_hip.so, see include/flicker_hip.h):
+
+  offline   s_j = sqrt(max_t|X[t,j]|) / sqrt(max_o|W[j,o]|), inv_s_j = 1/s_j  (calibration)
+            Wq = clamp(rint(W*s / w_o), +-127), w_o = max_j|W[j,o]*s_j| / 127   (per channel)
+  online    Xq = clamp(rint(X*inv_s / a_t), +-127), a_t = max_j|X[t,j]*inv_s_j| / 127
+            Y = bf16((f32(Xq . Wq) * a_t) * w_o)                                 (int32 GEMM)
+
+Typical use::
+
+    stats = absmax_cols(x_calib)                    # per input channel, over tokens
+    qw = quantize_linear(w, stats)                  # once per weight
+    y = linear(x, qw)                               # per forward: (..., K) -> (..., N) bf16
+"""
+
+from __future__ import annotations
+
+from typing import NamedTuple
+
+import torch
+
+from . import _lib
+from .kernels import _on_gpu
+
+
+class QuantizedLinear(NamedTuple):
+    """An int8 projection weight: ``wq_t`` (N, K) int8 is Wq transposed (k-contiguous
+    rows), ``w_scale`` (N,) f32 the per-channel scales, ``smooth`` / ``inv_smooth`` (K,)
+    f32 the SmoothQuant factors s and 1/s."""
+
+    wq_t: torch.Tensor
+    w_scale: torch.Tensor
+    smooth: torch.Tensor
+    inv_smooth: torch.Tensor
+
+    @property
+    def in_features(self) -> int:
+        return self.wq_t.shape[1]
+
+    @property
+    def out_features(self) -> int:
+        return self.wq_t.shape[0]
+
+
+def _rows(name: str, t: torch.Tensor) -> torch.Tensor:
+    """A 2-D bf16 view with a contiguous last axis and 16-byte aligned rows."""
+    _on_gpu(name, t)
+    if t.dtype != torch.bfloat16:
+        raise ValueError(f"{name} must be bfloat16, got {t.dtype}")
+    if t.dim() != 2:
+        t = t.reshape(-1, t.shape[-1])
+    if t.stride(-1) != 1 or t.stride(0) % 8 or t.data_ptr() % 16:
+        t = t.contiguous()
+    return t
+
+
+def _f32(name: str, t: torch.Tensor, n: int, device) -> torch.Tensor:
+    _on_gpu(name, t)
+    if t.shape != (n,):
+        raise ValueError(f"{name} must have shape ({n},), got {tuple(t.shape)}")
+    return t.to(device=device, dtype=torch.float32).contiguous()
+
+
+def absmax_rows(w: torch.Tensor) -> torch.Tensor:
+    """Per-row max |w| of a bf16 (K, N) weight: the max_o |W[j,o]| of the smoothing factor."""
+    w = _rows("w", w)
+    out = torch.empty(w.shape[0], dtype=torch.float32, device=w.device)
+    _lib.check(_lib.lib().flk_absmax_rows(w.data_ptr(), w.shape[0], w.shape[1], w.stride(0), out.data_ptr(),
+                                          _lib.stream_of(w)), "flk_absmax_rows")
+    return out
+
+
+def absmax_cols(x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Per-channel max |x| over all tokens of a bf16 (..., K) activation.  With ``out``, the
+    result is folded into it (running maximum over calibration batches)."""
+    x = _rows("x", x)
+    k = x.shape[1]
+    accumulate = out is not None
+    if out is None:
+        out = torch.empty(k, dtype=torch.float32, device=x.device)
+    elif out.shape != (k,) or out.dtype != torch.float32 or not out.is_contiguous() or out.device != x.device:
+        raise ValueError(f"out must be a contiguous float32 ({k},) tensor on {x.device}")
+    _lib.check(_lib.lib().flk_absmax_cols(x.data_ptr(), x.shape[0], k, x.stride(0), int(accumulate),
+                                          out.data_ptr(), _lib.stream_of(x)), "flk_absmax_cols")
+    return out
+
+
+def smooth_factors(x_absmax: torch.Tensor, w_absmax: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """(s, 1/s) with s_j = sqrt(x_absmax_j) / sqrt(w_absmax_j) (1 where either is 0)."""
+    k = x_absmax.shape[0]
+    xa = _f32("x_absmax", x_absmax, k, x_absmax.device)
+    wa = _f32("w_absmax", w_absmax, k, xa.device)
+    s = torch.empty_like(xa)
+    inv = torch.empty_like(xa)
+    _lib.check(_lib.lib().flk_smooth_factors(xa.data_ptr(), wa.data_ptr(), k, s.data_ptr(), inv.data_ptr(),
+                                             _lib.stream_of(xa)), "flk_smooth_factors")
+    return s, inv
+
+
+def quantize_weight(w: torch.Tensor, smooth: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """bf16 (K, N) weight and smoothing factors -> (wq_t (N, K) int8, w_scale (N,) f32)."""
+    w = _rows("w", w)
+    k, n = w.shape
+    s = _f32("smooth", smooth, k, w.device)
+    wq_t = torch.empty((n, k), dtype=torch.int8, device=w.device)
+    w_scale = torch.empty(n, dtype=torch.float32, device=w.device)
+    _lib.check(_lib.lib().flk_quantize_weight(w.data_ptr(), w.stride(0), s.data_ptr(), k, n, wq_t.data_ptr(),
+                                              w_scale.data_ptr(), _lib.stream_of(w)), "flk_quantize_weight")
+    return wq_t, w_scale
+
+
+def quantize_linear(w: torch.Tensor, x_absmax: torch.Tensor) -> QuantizedLinear:
+    """Offline half: smoothing factors from calibration statistics, then the int8 weight."""
+    s, inv = smooth_factors(x_absmax, absmax_rows(w))
+    wq_t, w_scale = quantize_weight(w, s)
+    return QuantizedLinear(wq_t, w_scale, s, inv)
+
+
+def quantize_act(x: torch.Tensor, inv_smooth: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """bf16 (..., K) activation -> (xq (M, K) int8, a_scale (M,) f32), M = prod(leading dims)."""
+    x = _rows("x", x)
+    m, k = x.shape
+    inv = _f32("inv_smooth", inv_smooth, k, x.device)
+    xq = torch.empty((m, k), dtype=torch.int8, device=x.device)
+    a_scale = torch.empty(m, dtype=torch.float32, device=x.device)
+    _lib.check(_lib.lib().flk_quantize_act(x.data_ptr(), x.stride(0), inv.data_ptr(), m, k, xq.data_ptr(),
+                                           a_scale.data_ptr(), _lib.stream_of(x)), "flk_quantize_act")
+    return xq, a_scale
+
+
+def gemm(xq: torch.Tensor, a_scale: torch.Tensor, wq_t: torch.Tensor, w_scale: torch.Tensor, *,
+         out: torch.Tensor | None = None, acc: torch.Tensor | None = None) -> torch.Tensor:
+    """Y (M, N) bf16 = bf16((f32(xq . wq_t^T) * a_scale) * w_scale).  ``out`` may be a row-strided
+    (M, N) view (e.g. the qkv columns of a wider buffer); ``acc`` (M, N) int32 receives the
+    exact integer products when given."""
+    for name, t in (("xq", xq), ("wq_t", wq_t)):
+        _on_gpu(name, t)
+        if t.dtype != torch.int8 or t.dim() != 2 or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous 2-D int8 tensor")
+    m, k = xq.shape
+    n = wq_t.shape[0]
+    if wq_t.shape[1] != k:
+        raise ValueError(f"xq has {k} input channels but wq_t has {wq_t.shape[1]}")
+    a = _f32("a_scale", a_scale, m, xq.device)
+    ws = _f32("w_scale", w_scale, n, xq.device)
+    if out is None:
+        out = torch.empty((m, n), dtype=torch.bfloat16, device=xq.device)
+    elif out.shape != (m, n) or out.dtype != torch.bfloat16 or out.stride(1) != 1:
+        raise ValueError(f"out must be a bfloat16 ({m}, {n}) view with contiguous rows")
+    if acc is not None and (acc.shape != (m, n) or acc.dtype != torch.int32 or not acc.is_contiguous()):
+        raise ValueError(f"acc must be a contiguous int32 ({m}, {n}) tensor")
+    _lib.check(_lib.lib().flk_w8a8_gemm(xq.data_ptr(), wq_t.data_ptr(), a.data_ptr(), ws.data_ptr(), m, k, n,
+                                        out.data_ptr(), out.stride(0), _lib.ptr(acc), _lib.stream_of(xq)),
+               "flk_w8a8_gemm")
+    return out
+
+
+def linear(x: torch.Tensor, qw: QuantizedLinear, *, out: torch.Tensor | None = None) -> torch.Tensor:
+    """int8 stand-in for ``linear(x, w)`` (nn.py:13-14): (..., K) bf16 -> (..., N) bf16."""
+    lead = x.shape[:-1]
+    xq, a_scale = quantize_act(x, qw.inv_smooth)
+    y = gemm(xq, a_scale, qw.wq_t, qw.w_scale, out=None if out is None else out.view(-1, qw.out_features))
+    return y.reshape(*lead, qw.out_features) if out is None else out

@@ -10,6 +10,10 @@ same values) and then moved:
   k_scale  (128,) bf16 = 1 + 0.05 N(0, 1)                             seed 2
   stress   a seeded 5% of the 9216 channels scaled by 8 (batch-4 case) seed 5
   ids      text (0, 0, 0, i) then image (0, row, col, 0)  (rope.py:33-45)
+
+The int8 QKV projection workload (``Projection``) is X (M, 3072) bf16 ~ N(0, 1) with a
+seeded 1% of the input channels scaled by 20 (activation outliers, the case SmoothQuant
+targets; seeds 3 and 5) and W (3072, 9216) bf16 ~ N(0, 0.02) (seed 4).
 """
 
 from __future__ import annotations
@@ -68,6 +72,29 @@ WORKLOADS = {
 }
 
 
+@dataclass(frozen=True)
+class Projection:
+    """One QKV projection: (tokens, hidden) x (hidden, 3 H D)."""
+
+    name: str
+    tokens: int
+    hidden: int = KLEIN.hidden_size
+    out_features: int = 3 * KLEIN.num_heads * KLEIN.head_dim
+    outlier_fraction: float = 0.01
+    outlier_gain: float = 20.0
+
+    def gemm_ops(self) -> int:
+        """2 M K N integer multiply-adds counted as two ops each."""
+        return 2 * self.tokens * self.hidden * self.out_features
+
+    def gemm_bytes(self) -> int:
+        """Algorithmic HBM bytes of one GEMM: int8 X and W once, bf16 Y written."""
+        return self.tokens * self.hidden + self.hidden * self.out_features + 2 * self.tokens * self.out_features
+
+
+PROJECTIONS = {p.name: p for p in (Projection("qkv_1024", 4608), Projection("qkv_512", 1536))}
+
+
 def _gen(seed: int) -> torch.Generator:
     return torch.Generator("cpu").manual_seed(seed)
 
@@ -95,3 +122,13 @@ def make_ids(w: Workload) -> np.ndarray:
 def q_gain(w: Workload) -> float:
     """dit.py:36 -- the bounded path pre-scales queries by 1/sqrt(head_dim)."""
     return 1.0 / math.sqrt(w.head_dim)
+
+
+def make_projection(p: Projection) -> tuple[torch.Tensor, torch.Tensor]:
+    """(X (M, K), W (K, N)) bf16 on the CPU: outlier channels in X, W ~ N(0, 0.02)."""
+    x = torch.randn((p.tokens, p.hidden), generator=_gen(3), dtype=torch.float32)
+    count = int(round(p.outlier_fraction * p.hidden))
+    picks = torch.randperm(p.hidden, generator=_gen(5))[:count]
+    x[:, picks] *= p.outlier_gain
+    w = 0.02 * torch.randn((p.hidden, p.out_features), generator=_gen(4), dtype=torch.float32)
+    return x.to(torch.bfloat16), w.to(torch.bfloat16)

@@ -88,6 +88,49 @@ int flk_lane_pair(const float* pe, int64_t length, int pairs, float* cos, float*
 int flk_rope_lanes(const float* ids, int64_t ids_row_stride, int64_t length, int n_axes,
                    const int* axes_dim, float theta, float* cos, float* sin, void* stream);
 
+/* ---- int8 SmoothQuant W8A8 QKV projection ------------------------------------------
+ * Replaces the bf16 projection `linear(x, w) = x @ w` (src/flicker/nn.py:13-14) where the
+ * reference calls it for the fused QKV projection (src/flicker/modules.py:128,132,186:
+ * img/txt qkv of double blocks, linear1 of single blocks).  The reference has no
+ * quantisation; the replacement is defined by this formula, reproduced bit for bit
+ * (single IEEE f32 operations, round-to-nearest-even, correctly rounded / and sqrt):
+ *   s_j  = sqrt(max_t|X[t,j]|) / sqrt(max_o|W[j,o]|)   (1 if either is 0), inv_s_j = 1/s_j
+ *   w_o  = max_j|f32(W[j,o])*s_j| / 127 (1 if 0);  Wq = clamp(rint(f32(W)*s_j / w_o), +-127)
+ *   a_t  = max_j|f32(X[t,j])*inv_s_j| / 127 (1 if 0);  Xq = clamp(rint(f32(X)*inv_s_j / a_t), +-127)
+ *   acc  = Xq . Wq (int32, exact);  Y = bf16((f32(acc) * a_t) * w_o)
+ * bf16 matrices are row-major with a row stride in elements. */
+
+/* Calibration: out[r] = max_c |x[r,c]| of a bf16 (rows, cols) matrix (cols % 8 == 0). */
+int flk_absmax_rows(const void* x, int64_t rows, int64_t cols, int64_t row_stride, float* out,
+                    void* stream);
+
+/* Calibration: out[c] = max_r |x[r,c]|; with accumulate != 0, max(out[c], ...) so the
+ * activation statistics of several calibration batches can be folded in. */
+int flk_absmax_cols(const void* x, int64_t rows, int64_t cols, int64_t row_stride, int accumulate,
+                    float* out, void* stream);
+
+/* s and inv_s (k,) f32 from the activation and weight channel maxima. */
+int flk_smooth_factors(const float* x_absmax, const float* w_absmax, int64_t k, float* s,
+                       float* inv_s, void* stream);
+
+/* Weight W (k, n) bf16 (the reference's (in, out) layout) -> wq_t (n, k) int8, stored
+ * transposed so GEMM operands are k-contiguous, and w_scale (n,) f32.  k % 64 == 0,
+ * n % 8 == 0. */
+int flk_quantize_weight(const void* w, int64_t w_row_stride, const float* s, int k, int n,
+                        int8_t* wq_t, float* w_scale, void* stream);
+
+/* Activation X (m, k) bf16 -> xq (m, k) int8 and a_scale (m,) f32 (per token).
+ * k % 8 == 0, k <= 8192. */
+int flk_quantize_act(const void* x, int64_t x_row_stride, const float* inv_s, int m, int k,
+                     int8_t* xq, float* a_scale, void* stream);
+
+/* y (m, n) bf16 = rescaled int8 product of xq (m, k) and wq_t (n, k); when acc_or_null is
+ * given, the exact int32 products are also written there as (m, n).  k % 128 == 0,
+ * n % 4 == 0, y 8-byte aligned with y_row_stride % 4 == 0. */
+int flk_w8a8_gemm(const int8_t* xq, const int8_t* wq_t, const float* a_scale, const float* w_scale,
+                  int m, int k, int n, void* y, int64_t y_row_stride, int32_t* acc_or_null,
+                  void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,219 @@
+"""int8 SmoothQuant W8A8 QKV projection on the GPU against the oracle (oracle/w8a8.py) and
+the golden brute force (tests/golden/w8a8.npz).  Everything here is integer work or single
+rounded f32 operations, so the bar is bit-exact: int8 operands, int32 accumulators, f32
+scales and the bf16 output must all match exactly."""
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from flicker_amd import w8a8, workloads
+from oracle import w8a8 as Q
+from oracle.numerics import bf16_bits, from_bf16_bits
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def host(t):
+    return t.detach().cpu().numpy()
+
+
+def host_f32(t):
+    return t.detach().to("cpu", torch.float32).numpy()
+
+
+def assert_bits_equal(got_bf16: torch.Tensor, want_f32: np.ndarray, label: str):
+    got = bf16_bits(host_f32(got_bf16))
+    want = bf16_bits(np.asarray(want_f32, np.float32))
+    bad = np.argwhere(got != want)
+    assert bad.size == 0, f"{label}: {len(bad)} of {got.size} differ, first at {bad[0].tolist()}"
+
+
+def test_golden_pipeline_bit_exact(device):
+    """The brute-force fixture (5 tokens, 16 -> 6 channels, one outlier channel, one zero
+    token), zero-padded to the kernels' k % 128 and n % 8: padding adds zero channels, which
+    leave every smoothing factor, scale and product of the real channels unchanged."""
+    g = np.load(os.path.join(GOLDEN, "w8a8.npz"))
+    x = from_bf16_bits(g["x"])
+    w = from_bf16_bits(g["w"])
+    m, k = x.shape
+    n = w.shape[1]
+    kp, np_ = 128, 8
+    xp = np.zeros((m, kp), np.float32)
+    xp[:, :k] = x
+    wp = np.zeros((kp, np_), np.float32)
+    wp[:k, :n] = w
+    xt = torch.from_numpy(xp).to(torch.bfloat16).to(device)
+    wt = torch.from_numpy(wp).to(torch.bfloat16).to(device)
+
+    qw = w8a8.quantize_linear(wt, w8a8.absmax_cols(xt))
+    np.testing.assert_array_equal(host(qw.smooth)[:k], g["smooth"])
+    np.testing.assert_array_equal(host(qw.inv_smooth)[:k], g["inv_smooth"])
+    np.testing.assert_array_equal(host(qw.w_scale)[:n], g["w_scale"])
+    np.testing.assert_array_equal(host(qw.wq_t)[:n, :k].T, g["wq"])
+
+    xq, a_scale = w8a8.quantize_act(xt, qw.inv_smooth)
+    np.testing.assert_array_equal(host(xq)[:, :k], g["xq"])
+    np.testing.assert_array_equal(host(a_scale), g["a_scale"])
+
+    acc = torch.empty((m, np_), dtype=torch.int32, device=device)
+    y = w8a8.gemm(xq, a_scale, qw.wq_t, qw.w_scale, acc=acc)
+    np.testing.assert_array_equal(host(acc)[:, :n], g["acc"])
+    np.testing.assert_array_equal(bf16_bits(host_f32(y))[:, :n], g["y"])
+
+
+def calib_inputs(m=777, k=320, n=264, seed=7):
+    """bf16 X with outlier channels, an all-zero channel and an all-zero token; bf16 W with an
+    all-zero input row."""
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn((m, k), generator=g)
+    x[:, 5] *= 30.0
+    x[:, 9] = 0.0
+    x[3] = 0.0
+    w = 0.02 * torch.randn((k, n), generator=g)
+    w[11] = 0.0
+    return x.to(torch.bfloat16), w.to(torch.bfloat16)
+
+
+def test_calibration_statistics_and_smoothing(device):
+    x, w = calib_inputs()
+    xn, wn = x.float().numpy(), w.float().numpy()
+    xa = w8a8.absmax_cols(x.to(device))
+    wa = w8a8.absmax_rows(w.to(device))
+    np.testing.assert_array_equal(host(xa), np.abs(xn).max(0))
+    np.testing.assert_array_equal(host(wa), np.abs(wn).max(1))
+    # running maximum over two calibration batches equals the maximum over their union
+    run = w8a8.absmax_cols(x[:400].to(device))
+    w8a8.absmax_cols(x[400:].to(device), out=run)
+    np.testing.assert_array_equal(host(run), np.abs(xn).max(0))
+    s, inv = w8a8.smooth_factors(xa, wa)
+    s_want = Q.smooth_factors(np.abs(xn).max(0), np.abs(wn).max(1))
+    np.testing.assert_array_equal(host(s), s_want)
+    np.testing.assert_array_equal(host(inv), Q.inverse(s_want))
+    assert host(s)[9] == 1.0 and host(s)[11] == 1.0       # zero activation / zero weight row
+
+
+def test_quantize_weight_full_size_bit_exact(device):
+    p = workloads.PROJECTIONS["qkv_1024"]
+    x, w = workloads.make_projection(p)
+    xa = np.abs(x.float().numpy()).max(0)
+    wn = w.float().numpy()
+    s = Q.smooth_factors(xa, np.abs(wn).max(1))
+    wq_want, ws_want = Q.quantize_weight(wn, s)
+    wq_t, ws = w8a8.quantize_weight(w.to(device), torch.from_numpy(s).to(device))
+    np.testing.assert_array_equal(host(ws), ws_want)
+    np.testing.assert_array_equal(host(wq_t), wq_want.T)
+
+
+@pytest.mark.parametrize("strided", [False, True])
+def test_quantize_act_bit_exact(device, strided):
+    p = workloads.PROJECTIONS["qkv_1024"]
+    x, _ = workloads.make_projection(p)
+    x[17] = 0.0                                                   # zero token: scale 1, all zeros
+    inv = Q.inverse(Q.smooth_factors(np.abs(x.float().numpy()).max(0) * 0.5 + 0.25,
+                                     np.full(p.hidden, 0.06, np.float32)))
+    xd = x.to(device)
+    if strided:                                                   # a column block of a wider activation
+        wide = torch.zeros((p.tokens, p.hidden + 512), dtype=torch.bfloat16, device=device)
+        wide[:, 256:256 + p.hidden] = xd
+        xd = wide[:, 256:256 + p.hidden]
+    xq, a = w8a8.quantize_act(xd, torch.from_numpy(inv).to(device))
+    xq_want, a_want = Q.quantize_act(x.float().numpy(), inv)
+    np.testing.assert_array_equal(host(a), a_want)
+    np.testing.assert_array_equal(host(xq), xq_want)
+    assert host(a)[17] == 1.0
+
+
+@pytest.mark.parametrize("m,k,n", [(300, 256, 520), (1, 128, 4), (257, 3072, 260), (512, 128, 1024), (4608, 3072, 9216 // 36)])
+def test_gemm_tails_bit_exact(device, m, k, n):
+    """Ragged tiles in both output dimensions; full-range int8 operands."""
+    rng = np.random.default_rng(m * 7 + n)
+    xq = rng.integers(-127, 128, (m, k), dtype=np.int8)
+    wq = rng.integers(-127, 128, (k, n), dtype=np.int8)
+    a = (rng.random(m, dtype=np.float32) * 0.05 + 1e-3).astype(np.float32)
+    ws = (rng.random(n, dtype=np.float32) * 0.002 + 1e-5).astype(np.float32)
+    acc = torch.empty((m, n), dtype=torch.int32, device=device)
+    y = w8a8.gemm(torch.from_numpy(xq).to(device), torch.from_numpy(a).to(device),
+                  torch.from_numpy(np.ascontiguousarray(wq.T)).to(device), torch.from_numpy(ws).to(device), acc=acc)
+    acc_want = Q.int_gemm(xq, wq)
+    np.testing.assert_array_equal(host(acc), acc_want)
+    assert_bits_equal(y, Q.rescale(acc_want, a, ws), f"y {m}x{k}x{n}")
+
+
+def test_gemm_extreme_operands(device):
+    """All operands at +-127: the largest |acc| the int32 accumulator sees at K = 3072."""
+    m, k, n = 64, 3072, 64
+    xq = np.full((m, k), 127, np.int8)
+    xq[1::2] = -127
+    wq = np.full((k, n), 127, np.int8)
+    acc = torch.empty((m, n), dtype=torch.int32, device=device)
+    w8a8.gemm(torch.from_numpy(xq).to(device), torch.ones(m, device=device),
+              torch.from_numpy(np.ascontiguousarray(wq.T)).to(device), torch.ones(n, device=device), acc=acc)
+    got = host(acc)
+    assert got[0, 0] == 3072 * 127 * 127 and got[1, 0] == -3072 * 127 * 127
+    np.testing.assert_array_equal(got, Q.int_gemm(xq, wq))
+
+
+def test_projection_full_size_bit_exact(device):
+    """The 1024^2 Klein QKV projection (4608 x 3072 -> 9216): calibrate on the input itself,
+    quantise, multiply; every int32 product and every bf16 output against the oracle."""
+    p = workloads.PROJECTIONS["qkv_1024"]
+    x, w = workloads.make_projection(p)
+    xd, wd = x.to(device), w.to(device)
+    qw = w8a8.quantize_linear(wd, w8a8.absmax_cols(xd))
+    xq, a = w8a8.quantize_act(xd, qw.inv_smooth)
+    acc = torch.empty((p.tokens, p.out_features), dtype=torch.int32, device=device)
+    y = w8a8.gemm(xq, a, qw.wq_t, qw.w_scale, acc=acc)
+
+    xn, wn = x.float().numpy(), w.float().numpy()
+    s = Q.smooth_factors(np.abs(xn).max(0), np.abs(wn).max(1))
+    wq_want, ws_want = Q.quantize_weight(wn, s)
+    y_want, acc_want, xq_want, a_want = Q.w8a8_linear(xn, Q.inverse(s), wq_want, ws_want)
+    np.testing.assert_array_equal(host(xq), xq_want)
+    np.testing.assert_array_equal(host(a), a_want)
+    np.testing.assert_array_equal(host(acc), acc_want)
+    assert_bits_equal(y, y_want, "y full projection")
+    # and the fused path (no acc written) gives the same output
+    y2 = w8a8.linear(xd, qw)
+    assert torch.equal(y2, y)
+
+
+def test_linear_writes_into_strided_output(device):
+    """Y written straight into the qkv columns of a wider (linear1-style) buffer."""
+    x, w = calib_inputs(m=130, k=256, n=384)
+    xd, wd = x.to(device), w.to(device)
+    qw = w8a8.quantize_linear(wd, w8a8.absmax_cols(xd))
+    wide = torch.full((130, 384 + 128), 7.0, dtype=torch.bfloat16, device=device)
+    w8a8.linear(xd, qw, out=wide[:, :384])
+    assert torch.equal(wide[:, :384], w8a8.linear(xd, qw))
+    assert bool((wide[:, 384:] == 7.0).all())
+
+
+def test_quantisation_error_against_bf16_projection(device):
+    """Sanity of the int8 replacement against the bf16 projection it stands in for
+    (nn.py:13-14): relative Frobenius error of a few percent on outlier-heavy activations."""
+    p = workloads.PROJECTIONS["qkv_512"]
+    x, w = workloads.make_projection(p)
+    xd, wd = x.to(device), w.to(device)
+    y = w8a8.linear(xd, w8a8.quantize_linear(wd, w8a8.absmax_cols(xd)))
+    ref = x.double().numpy() @ w.double().numpy()
+    rel = np.linalg.norm(host_f32(y) - ref) / np.linalg.norm(ref)
+    assert rel < 0.03, rel
+
+
+def test_errors(device):
+    x = torch.zeros((4, 100), dtype=torch.bfloat16, device=device)
+    with pytest.raises(Exception, match="status -3"):        # k % 8
+        w8a8.quantize_act(x[:, :98], torch.ones(98, device=device))
+    xq = torch.zeros((4, 96), dtype=torch.int8, device=device)
+    with pytest.raises(Exception, match="status -3"):        # k % 128
+        w8a8.gemm(xq, torch.ones(4, device=device), torch.zeros((8, 96), dtype=torch.int8, device=device),
+                  torch.ones(8, device=device))
+    with pytest.raises(ValueError, match="input channels"):
+        w8a8.gemm(xq, torch.ones(4, device=device), torch.zeros((8, 64), dtype=torch.int8, device=device),
+                  torch.ones(8, device=device))
+    with pytest.raises(ValueError, match="GPU"):
+        w8a8.quantize_act(torch.zeros((4, 64), dtype=torch.bfloat16), torch.ones(64))

@@ -177,3 +177,39 @@ def test_bench_refuses_multi_gpu():
     proc = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"],
                           capture_output=True, text=True, timeout=120)
     assert proc.returncode == 2 and "one GPU" in proc.stderr
+
+
+def test_w8a8_validation(lib):
+    assert lib.flk_w8a8_gemm(FAKE, FAKE, FAKE, FAKE, 64, 192, 64, FAKE, 64, None, None) == _lib.FLK_E_UNSUPPORTED
+    assert lib.flk_w8a8_gemm(FAKE, FAKE, FAKE, FAKE, 64, 256, 66, FAKE, 66, None, None) == _lib.FLK_E_UNSUPPORTED
+    assert lib.flk_w8a8_gemm(FAKE, FAKE, FAKE, FAKE, 64, 256, 64, FAKE, 32, None, None) == _lib.FLK_E_INVALID
+    assert lib.flk_w8a8_gemm(FAKE, FAKE, FAKE, FAKE, 64, 256, 64, FAKE + 4, 64, None, None) == _lib.FLK_E_ALIGN
+    assert lib.flk_w8a8_gemm(FAKE, FAKE, FAKE, FAKE, 64, 2 ** 20, 64, FAKE, 64, None, None) == _lib.FLK_E_UNSUPPORTED
+    assert lib.flk_w8a8_gemm(FAKE, FAKE, FAKE, FAKE, 0, 256, 64, FAKE, 64, None, None) == _lib.FLK_OK
+    assert lib.flk_quantize_act(FAKE, 3000, FAKE, 8, 3072, FAKE, FAKE, None) == _lib.FLK_E_INVALID
+    assert lib.flk_quantize_act(FAKE, 3076, FAKE, 8, 3076, FAKE, FAKE, None) == _lib.FLK_E_UNSUPPORTED
+    assert lib.flk_quantize_act(FAKE, 16384, FAKE, 8, 16384, FAKE, FAKE, None) == _lib.FLK_E_UNSUPPORTED
+    assert lib.flk_quantize_weight(FAKE, 9216, FAKE, 3000, 9216, FAKE, FAKE, None) == _lib.FLK_E_UNSUPPORTED
+    assert lib.flk_absmax_rows(FAKE, 4, 12, 12, FAKE, None) == _lib.FLK_E_ALIGN
+    assert lib.flk_absmax_cols(FAKE, 4, 16, 8, 0, FAKE, None) == _lib.FLK_E_INVALID
+    assert lib.flk_smooth_factors(FAKE, FAKE, -1, FAKE, FAKE, None) == _lib.FLK_E_INVALID
+
+
+def test_w8a8_python_errors():
+    from flicker_amd import w8a8
+    with pytest.raises(ValueError, match="GPU"):
+        w8a8.quantize_act(torch.zeros((4, 64), dtype=torch.bfloat16), torch.ones(64))
+    with pytest.raises(ValueError, match="GPU"):
+        w8a8.gemm(torch.zeros((4, 128), dtype=torch.int8), torch.ones(4), torch.zeros((8, 128), dtype=torch.int8),
+                  torch.ones(8))
+
+
+def test_projection_workload():
+    p = workloads.PROJECTIONS["qkv_1024"]
+    assert (p.tokens, p.hidden, p.out_features) == (4608, 3072, 9216)
+    assert p.gemm_ops() == 2 * 4608 * 3072 * 9216 == 260919263232
+    assert p.gemm_bytes() == 4608 * 3072 + 3072 * 9216 + 2 * 4608 * 9216
+    x, w = workloads.make_projection(workloads.PROJECTIONS["qkv_512"])
+    amax = x.float().abs().amax(0)
+    assert int((amax > 20).sum()) == round(0.01 * 3072)          # the outlier channels
+    assert abs(float(w.float().std()) - 0.02) < 1e-3
