@@ -1,68 +1,71 @@
 // attend: bounded flash attention on gfx950 bf16 MFMA.
 //
 // Semantics follow the reference kernel (src/flicker/kernels.py:105-145): for each
-// (b, h) and query i, over key tiles in order,
+// (b, h) and query i, over keys in order,
 //   S = q_i . k_j  (bf16 operands, f32 accumulate)     -- q arrives scaled by 1/sqrt(D)
 //   P = bf16(exp(S))                                  -- no running max: QK-norm bounds S
 //   l += f32(P);  acc += P * v_j                       (f32)
 //   o_i = bf16(acc / l)
 //
-// Formulation.  Each wave owns 64 queries (two 32-query column blocks) and computes the
-// transposed score tile S^T = K Q^T with v_mfma_f32_32x32x16_bf16 (A = K rows from LDS,
-// B = Q^T held in registers for the whole kernel).  In the 32x32 accumulator layout a
-// lane owns one query column and 16 key rows, so
+// Formulation.  Each wave owns 32 queries and computes the transposed score tile
+// S^T = K Q^T with v_mfma_f32_32x32x16_bf16 (A = K rows from LDS, B = Q^T held in
+// registers for the whole kernel).  In the 32x32 accumulator layout a lane owns one query
+// column and 16 key rows, so
 //   * exp / bf16 rounding / the row sum l are lane-local (l is reduced across the two
 //     lane halves once, in the epilogue), and
 //   * the rounded P registers are directly the B operand (keys x queries) of the second
 //     product O^T += V^T P^T -- no shuffle of P through LDS.
-// Every LDS operand read feeds two MFMAs (one per query block).  V stays row-major in
-// LDS; its transposed operand (d rows x 8 keys per lane) is fetched with two
-// ds_read_b64_tr_b16, whose 16-lane transpose hands lane 4a+b element b of source lanes
-// a, a+4, a+8, a+12 -- so source lane s points at key K0 + s/4, columns D0 + 4(s%4).
-// The 8 keys a lane receives follow the accumulator-row order of S^T, so the P
-// registers of lane half g line up with the V^T k-slots of the same half.
+// V stays row-major in LDS; its transposed operand (d rows x 8 keys per lane) is fetched
+// with two ds_read_b64_tr_b16, whose 16-lane transpose hands lane 4a+b element b of source
+// lanes a, a+4, a+8, a+12 -- so source lane s points at key K0 + s/4, columns D0 + 4(s%4).
+// The 8 keys a lane receives follow the accumulator-row order of S^T, so the P registers
+// of lane half g line up with the V^T k-slots of the same half.
 //
-// Staging.  K and V tiles (64 keys x 256 B each) go from global memory straight into
-// LDS with global_load_lds_dwordx4 (no registers): lane i of a wave instruction lands
-// at base + 16 i, so the XOR swizzle is applied by choosing which global chunk each
-// lane fetches.  Both tiles use chunk' = chunk ^ swz(row), swz = ((row&3)<<1)|((row>>2)&1),
-// which keeps every 8 consecutive K rows (b128 operand reads) and every group of 4 V
-// rows x 2 chunks (transpose reads) on distinct banks of the 32-bank LDS.
+// Schedule.  Keys are processed in units of 32 (one S^T accumulator).  Phase u issues 16
+// MFMAs -- the 8 of S(u+1) = K(u+1) Q^T, then the 8 of O^T += V(u-1)^T P(u-1)^T -- and
+// spreads the exp work of unit u over them, one element per MFMA (log2(e) multiply of
+// element n+2, exp of n+1, and on every second slot the bf16 pack and row sum of a pair).
+// At two waves per SIMD that VALU load hides under the matrix pipe.  Each MFMA's LDS
+// operand is read kLead slots ahead into a 4-deep register ring, and the packed P values
+// and row sums are tied to their slots so the compiler cannot batch them elsewhere.
 //
-// Pipeline.  A block of 8 waves (two per SIMD, 32 queries each) streams 64-key tiles,
-// two 32-key units per tile.  In the phase of unit u the wave
-// first issues all 16 LDS operand reads, then alternates each QK^T MFMA of unit u+1
-// with the exp / bf16 / row-sum VALU work of two elements of unit u (explicit schedule
-// fences keep that interleave), then runs the 16 PV MFMAs of unit u.  Tiles stream
-// through a 4-buffer ring: the copy of tile t+3 starts with tile t and is waited on two
-// tiles later.
-// Blocks are renumbered so that all query tiles of one head run on the same XCD
-// (hardware deals blocks round-robin over the 8 XCDs), keeping the head's K/V in one L2.
+// Staging.  K and V live in separate 4-deep rings of 64-key tiles (16 KiB each).
+// Iteration t (the exp work of units 2t, 2t+1) reads K tiles t, t+1 and V tiles t-1, t,
+// starts the copies of K tile t+3 and V tile t+2, and ends by waiting for the copies it
+// started one iteration earlier, then a block barrier.  Copies go from global memory straight into LDS with
+// global_load_lds_dwordx4 (no registers), issued from inline asm so the compiler does not
+// order later LDS reads behind them: lane i of a wave instruction lands at M0 + 16 i, so
+// the XOR swizzle chunk' = chunk ^ swz(row), swz = ((row&3)<<1)|((row>>2)&1), is applied by
+// choosing which global chunk each lane fetches.  It keeps every 8 consecutive K rows (b128
+// operand reads) and every group of 4 V rows x 2 chunks (transpose reads) on distinct banks.
+// The main loop is unrolled over the four ring positions, so every LDS address is a
+// per-lane constant plus an immediate offset.
+//
+// Blocks of 8 waves (two per SIMD) take 256 queries of one (b, h).  Blocks are renumbered
+// so that all query tiles of one head run on the same XCD (hardware deals blocks
+// round-robin over the 8 XCDs), keeping the head's K/V in one L2.
 
 #include "common.h"
 
 namespace {
 
-constexpr int kD = 128;                 // head dim
-#ifndef FLK_ATTEND_WAVES
-#define FLK_ATTEND_WAVES 8
-#endif
-#ifndef FLK_ATTEND_QB
-#define FLK_ATTEND_QB 1
-#endif
-constexpr int kWaves = FLK_ATTEND_WAVES;   // waves per block (two per SIMD at 8)
-constexpr int kQB = FLK_ATTEND_QB;         // 32-query column blocks per wave
-constexpr int kWavesPerSimd = kWaves / 4;
-constexpr int kRowsPerWave = 64 / kWaves;  // tile rows each wave copies
-constexpr int kBM = kWaves * kQB * 32;  // queries per block
-constexpr int kBN = 64;                 // keys per LDS tile (two 32-key units)
-constexpr int kStages = 4;
+constexpr int kD = 128;                  // head dim
+constexpr int kWaves = 8;                // waves per block, two per SIMD
+constexpr int kBM = kWaves * 32;         // queries per block
+constexpr int kBN = 64;                  // keys per LDS tile (two 32-key units)
+constexpr int kRing = 4;                 // tiles per ring (K and V each)
 constexpr int kThreads = kWaves * 64;
-constexpr int kRowBytes = kD * 2;       // one K or V row: 256 B = 16 chunks of 16 B
-constexpr int kTileBytes = kBN * kRowBytes;
-constexpr int kBufBytes = 2 * kTileBytes;  // K tile then V tile
+constexpr int kRowBytes = kD * 2;        // one K or V row: 256 B = 16 chunks of 16 B
 constexpr int kUnitBytes = 32 * kRowBytes;
+constexpr int kTileBytes = kBN * kRowBytes;
+constexpr int kVRing = kRing * kTileBytes;     // byte offset of the V ring
+constexpr int kSmemBytes = 2 * kRing * kTileBytes;
+constexpr int kRowsPerWave = kBN / kWaves;     // tile rows each wave copies (8)
+constexpr int kDmaPerTensor = kRowsPerWave / 4;  // copy instructions per wave per tile (2)
+constexpr int kDmaPerIter = 2 * kDmaPerTensor;   // K and V
 constexpr int kXcds = 8;
+constexpr int kLead = 3;                 // slots between an operand's LDS read and its MFMA
+constexpr int kOpRing = 4;               // operand registers in flight (> kLead)
 constexpr float kLog2e = 1.4426950408889634f;
 
 using flk::bf16x2;
@@ -70,176 +73,154 @@ using flk::bf16x8;
 using flk::f32x16;
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef short s16x8 __attribute__((ext_vector_type(8)));
-typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
 __device__ __forceinline__ int swz(int row) { return ((row & 3) << 1) | ((row >> 2) & 1); }
 
-// Copy one 64-key tile of K and V (rows kv0..kv0+63, clamped to the last row) into `buf`.
-// Each wave moves 64/kWaves rows of K and of V, 4 rows (64 lanes x 16 B) per instruction:
-// lane i of global_load_lds_dwordx4 lands at M0 + 16 i.  The instruction is issued from
-// inline asm so that the compiler does not order every later LDS read behind it (it cannot
-// prove the ring buffers disjoint); completion is awaited explicitly with vmcnt.
-constexpr int kDmaPerTile = 2 * (kRowsPerWave / 4);  // per wave: K and V instructions of one tile
-
-__device__ __forceinline__ void copy_tile(uint8_t* buf, const uint16_t* __restrict__ kh,
-                                          const uint16_t* __restrict__ vh, int kv0, int length,
-                                          int wave, int lane) {
-#pragma unroll
-  for (int i = 0; i < kRowsPerWave / 4; ++i) {
-    const int row0 = wave * kRowsPerWave + i * 4;               // wave-uniform first row
-    const int row = row0 + (lane >> 4);                          // tile row this lane fills
-    const int chunk = (lane & 15) ^ swz(row);                    // logical chunk for its slot
-    const int key = min(kv0 + row, length - 1);
-    const int64_t src = (int64_t)key * kD + chunk * 8;
-    flk::dma16(kh + src, buf + row0 * kRowBytes);
-    flk::dma16(vh + src, buf + kTileBytes + row0 * kRowBytes);
-  }
-}
-
 struct WaveState {
-  bf16x8 qreg[kQB][8];
-  f32x16 oacc[kQB][4];
-  f32x16 sA[kQB];
-  f32x16 sB[kQB];
-  float lsum[kQB];
-  int k_off[8];   // K operand byte offsets within a unit (d step st)
-  int v_off[4];   // V^T transpose-read byte offsets within a tile (d block m), key step 0
+  bf16x8 qreg[8];      // Q^T operand, d step st
+  f32x16 oacc[4];      // O^T, d block m
+  f32x16 sA, sB;       // S^T of consecutive units
+  uint32_t pA[8], pB[8];  // bf16x2-packed P of consecutive units
+  bf16x8 ops[kOpRing]; // operand ring: the A operand of MFMA slot n sits in ops[n % kOpRing]
+  float lsum;
+  int k_off[4];        // K operand byte offsets within a unit, d steps 0-3 (step st + 4 is
+                       // 8 chunks = 128 B further: the swizzle only permutes the low 3 chunk bits)
+  int v_off[4];        // V^T transpose-read byte offsets within a unit (d block m), key step 0
 };
 
-__device__ __forceinline__ bf16x8 v_operand(const uint8_t* vtile, int off) {
-  const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vtile + off));
-  const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vtile + off + 8 * kRowBytes));
+__device__ __forceinline__ bf16x8 v_operand(const uint8_t* vunit, int off) {
+  const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vunit + off));
+  const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vunit + off + 8 * kRowBytes));
   const s16x8 both = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
   return __builtin_bit_cast(bf16x8, both);
 }
 
-// exp / bf16 / row-sum of one element pair (two keys of one query).
-template <bool kMask>
-__device__ __forceinline__ uint32_t exp_pair(float s0, float s1, float& lsum, int key0, int length) {
-  float e0 = __builtin_amdgcn_exp2f(s0 * kLog2e);
-  float e1 = __builtin_amdgcn_exp2f(s1 * kLog2e);
-  if constexpr (kMask) {
-    e0 = key0 < length ? e0 : 0.0f;
-    e1 = key0 + 1 < length ? e1 : 0.0f;
-  }
-  const uint32_t w = flk::pack_bf16x2(e0, e1);
-  const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
-  lsum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w), ones, lsum, false);
-  return w;
+// Slot n of a phase issues one MFMA: n < 8 is step n of S = K Q^T (A = K row operand of
+// d step n), n >= 8 is step i = n - 8 of O^T += V^T P^T (A = V^T operand of key step i / 4,
+// d block i % 4).  Its A operand is read from LDS kLead slots earlier.
+__device__ __forceinline__ bf16x8 load_operand(const WaveState& w, int n, const uint8_t* k_unit,
+                                               const uint8_t* v_unit) {
+  if (n < 8) return *reinterpret_cast<const bf16x8*>(k_unit + w.k_off[n & 3] + (n >> 2) * 128);
+  const int i = n - 8;
+  return v_operand(v_unit, w.v_off[i & 3] + (i >> 2) * 16 * kRowBytes);
 }
 
-// Unit phase: P(u) = exp(S(u)) interleaved with S(u+1) = K(u+1) Q^T, then O^T += V(u)^T P(u)^T.
+// Phase u: S(u+1) = K(u+1) Q^T and O^T += V(u-1)^T P(u-1)^T on the MFMA pipe, while the VALU
+// turns S(u) into P(u) and l.  k_cur / v_cur hold K(u+1) and V(u-1); k_next holds K(u+2),
+// whose first kLead operands (those of the next phase) are read at the end of this one.
 template <bool kMask>
-__device__ __forceinline__ void unit_phase(WaveState& w, const f32x16 (&s_cur)[kQB],
-                                           f32x16 (&s_next)[kQB], const uint8_t* k_next,
-                                           const uint8_t* v_tile, int ks0, int key_base,
-                                           int length, int g) {
-  bf16x8 kop[8], vop[2][4];
-#pragma unroll
-  for (int st = 0; st < 8; ++st) kop[st] = *reinterpret_cast<const bf16x8*>(k_next + w.k_off[st]);
-#pragma unroll
-  for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-    for (int m = 0; m < 4; ++m) vop[ks][m] = v_operand(v_tile, w.v_off[m] + (ks0 + ks) * 16 * kRowBytes);
-  // S(u) may sit in accumulation registers (the MFMA wrote it there); moving it to VGPRs
-  // once here, with an empty asm that must see it in VGPRs, keeps the exp work below from
-  // reading accumulation registers element by element while the next MFMAs are in flight,
-  // which serialises each read behind the matrix pipe.
-  f32x16 sv[kQB];
-#pragma unroll
-  for (int qb = 0; qb < kQB; ++qb) {
-    sv[qb] = s_cur[qb];
-    asm volatile("" : "+v"(sv[qb]));
-  }
-  __builtin_amdgcn_sched_barrier(0);
-
-  // The exp work of the 8*kQB element pairs is software-pipelined across the MFMA slots:
-  // slot n carries the log2(e) multiplies of pair n+2, the exps of pair n+1 and the bf16
-  // pack + row sum of pair n, so no VALU op waits on the one just issued before it.
-  constexpr int kPairs = 8 * kQB;                     // pair n: query block n % kQB, elements 2*(n/kQB), +1
-  uint32_t p[kQB][8];
-  float t[kPairs][2], e[kPairs][2];
-  auto stage_mul = [&](int n) {
-    const int qb = n % kQB, i = 2 * (n / kQB);
-    t[n][0] = sv[qb][i] * kLog2e;
-    t[n][1] = sv[qb][i + 1] * kLog2e;
-  };
-  auto stage_exp = [&](int n) {
-    e[n][0] = __builtin_amdgcn_exp2f(t[n][0]);
-    e[n][1] = __builtin_amdgcn_exp2f(t[n][1]);
-  };
-  auto stage_pack = [&](int n) {
-    const int qb = n % kQB, i = 2 * (n / kQB);
-    float e0 = e[n][0], e1 = e[n][1];
+__device__ __forceinline__ void phase(WaveState& w, const f32x16& s_cur, f32x16& s_next,
+                                      const uint32_t (&p_prev)[8], uint32_t (&p_cur)[8],
+                                      const uint8_t* k_cur, const uint8_t* v_cur, const uint8_t* k_next,
+                                      int key_base, int length, int g) {
+  f32x16 sv = s_cur;
+  asm volatile("" : "+v"(sv));
+  float t[16], e[16];
+  auto mul = [&](int n) { t[n] = sv[n] * kLog2e; };
+  auto ex = [&](int n) { e[n] = __builtin_amdgcn_exp2f(t[n]); };
+  auto pack = [&](int n) {  // elements n, n+1 -> p_cur[n/2]
+    float e0 = e[n], e1 = e[n + 1];
     if constexpr (kMask) {
-      const int key0 = key_base + (i >> 2) * 8 + g * 4 + (i & 3);
+      const int key0 = key_base + (n >> 2) * 8 + g * 4 + (n & 3);
       e0 = key0 < length ? e0 : 0.0f;
       e1 = key0 + 1 < length ? e1 : 0.0f;
     }
-    const uint32_t wv = flk::pack_bf16x2(e0, e1);
-    p[qb][i >> 1] = wv;
-    const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
-    w.lsum[qb] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, wv), ones, w.lsum[qb], false);
+    p_cur[n >> 1] = flk::pack_bf16x2(e0, e1);
+    asm volatile("" : "+v"(p_cur[n >> 1]));   // keep the pack in its MFMA slot
   };
-#pragma unroll
-  for (int qb = 0; qb < kQB; ++qb) s_next[qb] = f32x16{};
-  stage_mul(0);
-  stage_mul(1);
-  stage_exp(0);
+  auto rowsum = [&](int j) {  // l += both halves of p_cur[j] (issued a slot after its pack)
+    const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
+    w.lsum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, p_cur[j]), ones, w.lsum, false);
+    asm volatile("" : "+v"(w.lsum));   // pinned here: l feeds only the epilogue, so it would sink
+  };
+  const bf16x8 pb0 = __builtin_bit_cast(bf16x8, make_uint4(p_prev[0], p_prev[1], p_prev[2], p_prev[3]));
+  const bf16x8 pb1 = __builtin_bit_cast(bf16x8, make_uint4(p_prev[4], p_prev[5], p_prev[6], p_prev[7]));
+
+  mul(0);
+  mul(1);
+  ex(0);
+  s_next = f32x16{};
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int n = 0; n < kPairs; ++n) {
-    const int st = n / kQB, qb = n % kQB;              // the MFMA of this slot
-    s_next[qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop[st], w.qreg[qb][st], s_next[qb], 0, 0, 0);
-    if (n + 2 < kPairs) stage_mul(n + 2);
-    if (n + 1 < kPairs) stage_exp(n + 1);
-    stage_pack(n);
+  for (int n = 0; n < 16; ++n) {
+    bf16x8& a = w.ops[n % kOpRing];
+    if (n < 8) {
+      s_next = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, w.qreg[n], s_next, 0, 0, 0);
+    } else {
+      const int i = n - 8;
+      w.oacc[i & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, (i >> 2) ? pb1 : pb0, w.oacc[i & 3], 0, 0, 0);
+    }
+    const int nl = n + kLead;   // slot whose operand is read now
+    if (nl < 16) w.ops[nl % kOpRing] = load_operand(w, nl, k_cur, v_cur);
+    else w.ops[(nl - 16) % kOpRing] = load_operand(w, nl - 16, k_next, v_cur);
+    if (n + 2 < 16) mul(n + 2);
+    if (n + 1 < 16) ex(n + 1);
+    if (n & 1) pack(n - 1);
+    else if (n) rowsum((n >> 1) - 1);
+    if (n == 15) rowsum(7);
     __builtin_amdgcn_sched_barrier(0);
   }
+}
+
+// Copy 64-key tile `tile` (clamped to the last one) of K or V into an LDS ring slot.
+// Rows past the end of the sequence repeat the last row; those keys are masked.
+struct CopyPlan {
+  uint32_t voff[kDmaPerTensor];       // per-lane source offsets of a full tile
+  uint32_t voff_last[kDmaPerTensor];  // ... of the last tile (rows past the end repeat the last row)
+  int last_tile;                      // index of the last tile
+  int lds_wave_off;                   // this wave's rows within a tile (bytes, wave-uniform)
+};
+
+__device__ __forceinline__ void copy_tile(uint8_t* dst, const uint16_t* __restrict__ head, int tile,
+                                          const CopyPlan& cp) {
+  tile = min(tile, cp.last_tile);
+  const uint16_t* base = head + (int64_t)tile * kBN * kD;
+  if (tile < cp.last_tile) {
 #pragma unroll
-  for (int ks = 0; ks < 2; ++ks) {
-    bf16x8 b[kQB];
+    for (int i = 0; i < kDmaPerTensor; ++i) flk::dma16_at(base, cp.voff[i], dst + cp.lds_wave_off + i * 4 * kRowBytes);
+  } else {
 #pragma unroll
-    for (int qb = 0; qb < kQB; ++qb)
-      b[qb] = __builtin_bit_cast(bf16x8, make_uint4(p[qb][ks * 4], p[qb][ks * 4 + 1],
-                                                    p[qb][ks * 4 + 2], p[qb][ks * 4 + 3]));
-#pragma unroll
-    for (int m = 0; m < 4; ++m)
-#pragma unroll
-      for (int qb = 0; qb < kQB; ++qb)
-        w.oacc[qb][m] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vop[ks][m], b[qb], w.oacc[qb][m], 0, 0, 0);
+    for (int i = 0; i < kDmaPerTensor; ++i)
+      flk::dma16_at(base, cp.voff_last[i], dst + cp.lds_wave_off + i * 4 * kRowBytes);
   }
 }
 
-// One 64-key tile = two unit phases.  The second phase computes S of the next tile's first
-// unit (on the last tile it reads a stale buffer; that result is unused).
+struct Ctx {
+  uint8_t* smem;
+  const uint16_t* kh;
+  const uint16_t* vh;
+  int length, ntiles, g;
+  CopyPlan cp;
+};
+
+// Iteration t at ring position r = t % 4: the exp work of units 2t and 2t+1.  It reads K
+// tiles t and t+1 and V tiles t-1 and t, and starts the copies of K tile t+3 and V tile
+// t+2 into the slots of K tile t-1 and V tile t-2, which no read of this iteration touches.
+// Called with a literal r in the unrolled main loop, so every LDS address folds to a
+// per-lane constant plus an immediate offset.
 template <bool kMask>
-__device__ __forceinline__ void tile_step(WaveState& w, const uint8_t* cur, const uint8_t* nxt,
-                                          int kv0, int length, int g) {
-  unit_phase<kMask>(w, w.sA, w.sB, cur + kUnitBytes, cur + kTileBytes, 0, kv0, length, g);
-  __builtin_amdgcn_sched_barrier(0);
-  unit_phase<kMask>(w, w.sB, w.sA, nxt, cur + kTileBytes, 2, kv0 + 32, length, g);
-  __builtin_amdgcn_sched_barrier(0);
+__device__ __forceinline__ void iteration(WaveState& w, const Ctx& c, int t, int r) {
+  copy_tile(c.smem + ((r + 3) & 3) * kTileBytes, c.kh, t + 3, c.cp);
+  copy_tile(c.smem + kVRing + ((r + 2) & 3) * kTileBytes, c.vh, t + 2, c.cp);
+  const uint8_t* k_t = c.smem + r * kTileBytes;                          // K tile t
+  const uint8_t* k_t1 = c.smem + ((r + 1) & 3) * kTileBytes;             // K tile t+1
+  const uint8_t* v_t = c.smem + kVRing + r * kTileBytes;                 // V tile t
+  const uint8_t* v_tm1 = c.smem + kVRing + ((r + 3) & 3) * kTileBytes;   // V tile t-1
+  const int key0 = t * kBN;
+  // phase 2t: K(2t+1), V(2t-1), next K(2t+2); phase 2t+1: K(2t+2), V(2t), next K(2t+3)
+  phase<kMask>(w, w.sA, w.sB, w.pB, w.pA, k_t + kUnitBytes, v_tm1 + kUnitBytes, k_t1, key0, c.length, c.g);
+  phase<kMask>(w, w.sB, w.sA, w.pA, w.pB, k_t1, v_t, k_t1 + kUnitBytes, key0 + 32, c.length, c.g);
+  // Wait for the copies started one iteration ago, then a plain s_barrier: the LDS reads
+  // still in flight touch no buffer the next copies write, so no lgkmcnt wait is needed.
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" :: "n"(kDmaPerIter) : "memory");
 }
 
-__device__ __forceinline__ void qk_first(WaveState& w, const uint8_t* kunit) {
-#pragma unroll
-  for (int qb = 0; qb < kQB; ++qb) w.sA[qb] = f32x16{};
-#pragma unroll
-  for (int st = 0; st < 8; ++st) {
-    const bf16x8 a = *reinterpret_cast<const bf16x8*>(kunit + w.k_off[st]);
-#pragma unroll
-    for (int qb = 0; qb < kQB; ++qb)
-      w.sA[qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, w.qreg[qb][st], w.sA[qb], 0, 0, 0);
-  }
-}
-
-__global__ __launch_bounds__(kThreads, kWavesPerSimd) void attend_kernel(
+__global__ __launch_bounds__(kThreads, 2) void attend_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, uint16_t* __restrict__ o, int length, int q_blocks,
     int total_blocks) {
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[kStages * kBufBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[kSmemBytes];
 
   // XCD-aware renumbering: hardware block id p runs on XCD p % 8; give each XCD a
   // contiguous range of logical ids (head-major), so a head's query tiles share an L2.
@@ -251,91 +232,122 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void attend_kernel(
   const int qblk = logical - bh * q_blocks;
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
-  const int lane = tid & 63;
-  const int g = lane >> 5;   // lane half: selects k-slots 8g..8g+7 and accumulator rows 4g..
-  const int c = lane & 31;   // query column (S^T, O^T) / operand row (K, V^T)
+  const int wave = tid >> 6, lane = tid & 63;
+  Ctx c;
+  c.smem = smem;
+  c.g = lane >> 5;            // lane half: selects k-slots 8g..8g+7 and accumulator rows 4g..
+  const int col = lane & 31;  // query column (S^T, O^T) / operand row (K, V^T)
+  c.length = length;
+  c.ntiles = (length + kBN - 1) / kBN;
+  c.cp.last_tile = c.ntiles - 1;
+  c.cp.lds_wave_off = __builtin_amdgcn_readfirstlane(wave * kRowsPerWave * kRowBytes);
+  {
+    const int rows_last = length - c.cp.last_tile * kBN;   // 1..64 valid rows in the last tile
+#pragma unroll
+    for (int i = 0; i < kDmaPerTensor; ++i) {
+      const int row = wave * kRowsPerWave + i * 4 + (lane >> 4);
+      const uint32_t chunk_off = ((lane & 15) ^ swz(row)) << 4;   // slot (lane & 15) holds this chunk
+      c.cp.voff[i] = (uint32_t)(row * kRowBytes) + chunk_off;
+      c.cp.voff_last[i] = (uint32_t)(min(row, rows_last - 1) * kRowBytes) + chunk_off;
+    }
+  }
 
   const int64_t head_off = (int64_t)bh * length * kD;
   const uint16_t* qh = q + head_off;
-  const uint16_t* kh = k + head_off;
-  const uint16_t* vh = v + head_off;
+  c.kh = k + head_off;
+  c.vh = v + head_off;
 
-  const int ntiles = (length + kBN - 1) / kBN;
-  const int full_tiles = length / kBN;
-  copy_tile(smem, kh, vh, 0, length, wave, lane);
-  copy_tile(smem + kBufBytes, kh, vh, kBN, length, wave, lane);
-  copy_tile(smem + 2 * kBufBytes, kh, vh, 2 * kBN, length, wave, lane);
+  // Prologue copies: K tiles 0-2, V tiles 0-1.
+  for (int tl = 0; tl < 3; ++tl) copy_tile(smem + tl * kTileBytes, c.kh, tl, c.cp);
+  for (int tl = 0; tl < 2; ++tl) copy_tile(smem + kVRing + tl * kTileBytes, c.vh, tl, c.cp);
 
   WaveState w;
-  const int q0 = qblk * kBM + wave * (kQB * 32);
+  const int q0 = qblk * kBM + wave * 32;
+  const int qi = q0 + col;
 #pragma unroll
-  for (int qb = 0; qb < kQB; ++qb) {
-    const int qi = q0 + qb * 32 + c;
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      w.qreg[qb][s] = qi < length
-                          ? *reinterpret_cast<const bf16x8*>(qh + (int64_t)qi * kD + s * 16 + g * 8)
-                          : bf16x8{};
-    }
-#pragma unroll
-    for (int m = 0; m < 4; ++m) w.oacc[qb][m] = f32x16{};
-    w.lsum[qb] = 0.0f;
+  for (int s = 0; s < 8; ++s) {
+    w.qreg[s] = qi < length ? *reinterpret_cast<const bf16x8*>(qh + (int64_t)qi * kD + s * 16 + c.g * 8)
+                            : bf16x8{};
   }
 #pragma unroll
-  for (int s = 0; s < 8; ++s) w.k_off[s] = c * kRowBytes + ((((s << 1) | g) ^ swz(c)) << 4);
+  for (int m = 0; m < 4; ++m) w.oacc[m] = f32x16{};
+  w.lsum = 0.0f;
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    w.k_off[s] = col * kRowBytes + ((((s << 1) | c.g) ^ swz(col)) << 4);
+    asm volatile("" : "+v"(w.k_off[s]));
+  }
   {
     // Transpose-read source lane: 16-lane block h, lane sl in it -> key g*4 + sl/4 (+16 ks,
     // +8 for the upper four k-slots), columns m*32 + 16*(h&1) + 4*(sl&3) .. +3.
     const int h = lane >> 4, sl = lane & 15;
-    const int key = g * 4 + (sl >> 2);
+    const int key = c.g * 4 + (sl >> 2);
     const int half = sl & 1;
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
       const int chunk = 4 * m + 2 * (h & 1) + ((sl & 3) >> 1);
       w.v_off[m] = key * kRowBytes + ((chunk ^ swz(key)) << 4) + half * 8;
+      // Opaque to the compiler: it then adds the (immediate) unit offsets with the DS
+      // instruction's offset field instead of a v_or per read.
+      asm volatile("" : "+v"(w.v_off[m]));
     }
   }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) w.pB[i] = 0u;   // P(-1) = 0: phase 0's PV MFMAs add nothing
+  // ... and the V(-1) operand they read (V ring slot 3, unit 1) is zeroed, so 0 * V = 0.
+  reinterpret_cast<uint4*>(smem + kVRing + 3 * kTileBytes + kUnitBytes)[tid] = make_uint4(0, 0, 0, 0);
 
-  asm volatile("s_waitcnt vmcnt(%0)" :: "n"(kDmaPerTile) : "memory");  // tiles 0 and 1 landed
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
-  qk_first(w, smem);
 
-  // Full tiles, then the partial tail tile (if any) with key masking.  Tile t lives in
-  // buffer t % 4.  Iteration t starts the copy of tile t + 3 (into the buffer tile t - 1 has
-  // left) and ends by waiting for all but that copy -- i.e. for tile t + 2, which the next
-  // iteration's second phase reads -- so each copy has two iterations to land.  Copies past
-  // the end re-read the last row into a buffer nobody reads.
-  for (int t = 0; t < full_tiles; ++t) {
-    copy_tile(smem + ((t + 3) & 3) * kBufBytes, kh, vh, (t + 3) * kBN, length, wave, lane);
-    tile_step<false>(w, smem + (t & 3) * kBufBytes, smem + ((t + 1) & 3) * kBufBytes, t * kBN, length, g);
-    asm volatile("s_waitcnt vmcnt(%0)" :: "n"(kDmaPerTile) : "memory");
-    __syncthreads();
+  // S(0) from K unit 0; operands of phase 0: K(1) and a placeholder V (multiplied by P(-1) = 0).
+  w.sA = f32x16{};
+#pragma unroll
+  for (int st = 0; st < 8; ++st) {
+    const bf16x8 a = *reinterpret_cast<const bf16x8*>(smem + w.k_off[st & 3] + (st >> 2) * 128);
+    w.sA = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, w.qreg[st], w.sA, 0, 0, 0);
   }
-  if (full_tiles < ntiles) {
-    const int t = full_tiles;
-    tile_step<true>(w, smem + (t & 3) * kBufBytes, smem + ((t + 1) & 3) * kBufBytes, t * kBN, length, g);
+#pragma unroll
+  for (int n = 0; n < kLead; ++n) w.ops[n % kOpRing] = load_operand(w, n, smem + kUnitBytes, smem);
+
+  // Unrolled main loop over full tiles, then the remaining (at most 3 full and one partial)
+  // tiles with key masking and a computed ring position.
+  const int full_tiles = length / kBN;
+  int t = 0;
+  for (; t + 4 <= full_tiles; t += 4) {
+    iteration<false>(w, c, t, 0);
+    iteration<false>(w, c, t + 1, 1);
+    iteration<false>(w, c, t + 2, 2);
+    iteration<false>(w, c, t + 3, 3);
   }
+  for (; t < c.ntiles; ++t) iteration<true>(w, c, t, t & 3);
   // No copy may still be writing this block's LDS when the block ends.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
+  // Drain: O^T += V(U-1)^T P(U-1)^T for the last unit (unit 1 of the last tile).
+  {
+    const uint8_t* v_last = smem + kVRing + ((c.ntiles - 1) & 3) * kTileBytes + kUnitBytes;
+    const bf16x8 pb0 = __builtin_bit_cast(bf16x8, make_uint4(w.pB[0], w.pB[1], w.pB[2], w.pB[3]));
+    const bf16x8 pb1 = __builtin_bit_cast(bf16x8, make_uint4(w.pB[4], w.pB[5], w.pB[6], w.pB[7]));
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      w.oacc[i & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(load_operand(w, 8 + i, v_last, v_last),
+                                                              (i >> 2) ? pb1 : pb0, w.oacc[i & 3], 0, 0, 0);
+  }
+
   // Epilogue: l over both lane halves, O = bf16(acc / l), 4 d values per 8-byte store.
+  const float l = w.lsum + __shfl_xor(w.lsum, 32);
+  if (qi < length) {
+    uint16_t* orow = o + head_off + (int64_t)qi * kD;
 #pragma unroll
-  for (int qb = 0; qb < kQB; ++qb) {
-    const float l = w.lsum[qb] + __shfl_xor(w.lsum[qb], 32);
-    const int qi = q0 + qb * 32 + c;
-    if (qi < length) {
-      uint16_t* orow = o + head_off + (int64_t)qi * kD;
+    for (int m = 0; m < 4; ++m) {
 #pragma unroll
-      for (int m = 0; m < 4; ++m) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int d0 = m * 32 + r * 8 + g * 4;
-          uint2 val;
-          val.x = flk::pack_bf16x2(w.oacc[qb][m][r * 4 + 0] / l, w.oacc[qb][m][r * 4 + 1] / l);
-          val.y = flk::pack_bf16x2(w.oacc[qb][m][r * 4 + 2] / l, w.oacc[qb][m][r * 4 + 3] / l);
-          *reinterpret_cast<uint2*>(orow + d0) = val;
-        }
+      for (int r = 0; r < 4; ++r) {
+        const int d0 = m * 32 + r * 8 + c.g * 4;
+        uint2 val;
+        val.x = flk::pack_bf16x2(w.oacc[m][r * 4 + 0] / l, w.oacc[m][r * 4 + 1] / l);
+        val.y = flk::pack_bf16x2(w.oacc[m][r * 4 + 2] / l, w.oacc[m][r * 4 + 3] / l);
+        *reinterpret_cast<uint2*>(orow + d0) = val;
       }
     }
   }
