@@ -4,9 +4,11 @@ One step = fused qk_prep on a (B, L, 9216) bf16 QKV activation followed by bound
 attention on its output, at the Klein 4B 1024^2 shape by default (512 text + 64x64
 image tokens = 4608, 24 heads x 128).  Inputs are resident in HBM before timing.
 
-Each kernel is bracketed by HIP events on the stream it is launched on (torch's
-current stream); `value` is attend's TFLOP/s over its own launches, and the line also
-reports qk_prep's GB/s and both roofline fractions.  To keep the QKV input from being
+The timed region is `--steps` steps (qk_prep then attend) between two HIP events on the
+launch stream (torch's current stream) -> ms_per_step.  Each kernel is then timed alone the
+same way, `--steps` back-to-back launches over the same rotating buffers, which gives its
+average launch duration: `value` is attend's TFLOP/s from that, and the line also reports
+qk_prep's GB/s and both roofline fractions.  To keep the QKV input from being
 served by the 256 MB Infinity Cache between steps, steps rotate over buffer sets
 whose total exceeds it.  A CPU baseline (the torch-CPU restatement of the reference's
 plain-XLA path, the oracle) is timed on the host cores.
@@ -31,6 +33,7 @@ import time
 
 HBM_PEAK_GBS = 8000.0           # MI355X HBM3E, GB/s
 BF16_DENSE_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, TFLOP/s
+INT8_DENSE_PEAK_TOPS = 5000.0    # MI355X dense int8 MFMA, TOP/s
 METRIC = "attend TFLOP/s + qk_prep GB/s at 1024² Klein shape; % of MI355X roofline"
 INFINITY_CACHE_BYTES = 256 * 2 ** 20
 ROOT = os.path.dirname(os.path.abspath(__file__))
@@ -45,6 +48,8 @@ def parse():
                     help="untimed steps; enough (~0.1 s) to bring the GPU to its working clock")
     ap.add_argument("--workload", default="klein_1024")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-w8a8", action="store_true", help="skip the int8 W8A8 QKV projection leg")
+    ap.add_argument("--projection", default="qkv_1024")
     ap.add_argument("--cpu-reps", type=int, default=3)
     ap.add_argument("--only", choices=["step", "calibrate"], default="step",
                     help="calibrate: the step plus a plain device copy of known size, for counter runs")
@@ -116,6 +121,33 @@ def cpu_baseline(w, qkv, qs, ks, ids, reps: int) -> dict:
                       f"p50 of {reps} after 1 warm-up"}
 
 
+def w8a8_leg(args, timed, dev) -> dict:
+    """The int8 SmoothQuant QKV projection feeding qk_prep (X (M, 3072) -> Y (M, 9216)):
+    activation quantisation and the int8-MFMA GEMM, each timed back to back."""
+    import torch
+
+    from flicker_amd import w8a8, workloads
+
+    p = workloads.PROJECTIONS[args.projection]
+    x_cpu, w_cpu = workloads.make_projection(p)
+    x, wt = x_cpu.to(dev), w_cpu.to(dev)
+    qw = w8a8.quantize_linear(wt, w8a8.absmax_cols(x))
+    xq, a_scale = w8a8.quantize_act(x, qw.inv_smooth)
+    ys = [torch.empty((p.tokens, p.out_features), dtype=torch.bfloat16, device=dev) for _ in range(2)]
+    for i in range(20):
+        w8a8.gemm(xq, a_scale, qw.wq_t, qw.w_scale, out=ys[i % 2])
+    gemm_ms = timed(lambda i: w8a8.gemm(xq, a_scale, qw.wq_t, qw.w_scale, out=ys[i % 2]), args.steps)
+    quant_ms = timed(lambda i: w8a8.quantize_act(x, qw.inv_smooth), args.steps)
+    tops = p.gemm_ops() / (gemm_ms * 1e-3) / 1e12
+    return {"workload": f"{p.name}: X ({p.tokens}, {p.hidden}) bf16 with {p.outlier_fraction:.0%} outlier "
+                        f"channels x{p.outlier_gain:g}, W ({p.hidden}, {p.out_features}) ~ N(0, 0.02)",
+            "roofline": {"bound": "mfma", "achieved": round(tops, 1), "peak": INT8_DENSE_PEAK_TOPS,
+                         "unit": "TOP/s", "frac": round(tops / INT8_DENSE_PEAK_TOPS, 4), "kernel": "w8a8_gemm_kernel",
+                         "ops_per_launch": p.gemm_ops(), "avg_launch_us": round(gemm_ms * 1e3, 2)},
+            "quantize_act_us": round(quant_ms * 1e3, 2),
+            "dtype": "int8 operands, int32 accumulate, bf16 out"}
+
+
 def main() -> int:
     args = parse()
     if args.ingest_pmc:
@@ -159,32 +191,40 @@ def main() -> int:
             copies.append((torch.empty(COPY_BYTES, dtype=torch.uint8, device=dev).fill_(1),
                            torch.empty(COPY_BYTES, dtype=torch.uint8, device=dev)))
 
-    def step(i, ev=None):
-        qkv, out, o = sets[i % n_sets]
-        if ev is not None:
-            ev[0].record()
+    def run_qk(i):
+        qkv, out, _ = sets[i % n_sets]
         kernels.qk_prep(qkv, qs, ks, freqs, w.num_heads, out=out)
-        if ev is not None:
-            ev[1].record()
+
+    def run_attend(i):
+        _, out, o = sets[i % n_sets]
         kernels.attend(*out, out=o)
-        if ev is not None:
-            ev[2].record()
+
+    def step(i):
+        run_qk(i)
+        run_attend(i)
         if copies:
             src, dst = copies[i % len(copies)]
             dst.copy_(src)
 
+    def timed(fn, n):
+        """Average ms per call of n back-to-back calls between one pair of HIP events on the
+        launch stream (torch's current stream, which the kernels are enqueued on)."""
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(n):
+            fn(i)
+        e1.record()
+        e1.synchronize()
+        return e0.elapsed_time(e1) / n
+
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
-    events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        step(i, events[i])
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-
-    qk_ms = sum(e[0].elapsed_time(e[1]) for e in events) / args.steps
-    at_ms = sum(e[1].elapsed_time(e[2]) for e in events) / args.steps
+    step_ms = timed(step, args.steps)
+    # Per-kernel launch durations: each kernel alone, back to back over the same rotating
+    # buffers (what a rocprofv3 kernel trace of the same command reports per dispatch).
+    qk_ms = timed(run_qk, args.steps) if args.only == "step" else step_ms
+    at_ms = timed(run_attend, args.steps) if args.only == "step" else step_ms
     qk_gbs = w.qk_prep_bytes() / (qk_ms * 1e-3) / 1e9
     at_tflops = w.attend_flops() / (at_ms * 1e-3) / 1e12
 
@@ -201,7 +241,7 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(wall * 1e3 / args.steps, 4),
+        "ms_per_step": round(step_ms, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -222,6 +262,8 @@ def main() -> int:
                                  "traffic_source": source, "kernel": "qk_prep_kernel",
                                  "bytes_per_launch": w.qk_prep_bytes(), "avg_launch_us": round(qk_ms * 1e3, 2)}},
     }
+    if not args.no_w8a8 and args.only == "step":
+        result["w8a8"] = w8a8_leg(args, timed, dev)
     if not args.no_cpu_baseline and args.only == "step":
         result["cpu_baseline"] = cpu_baseline(w, qkv_cpu, qs_cpu, ks_cpu, ids, args.cpu_reps)
     print(json.dumps(result), flush=True)
