@@ -23,6 +23,7 @@ SIGNATURES = {
     "flk_qk_prep": (_i, [_p, _i64, _i64, _p, _p, _i64, _p, _p, _i, _f, _i, _i, _i, _i,
                          _p, _p, _p, _i64, _i64, _p]),
     "flk_attend": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _p]),
+    "flk_attend_to": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _i64, _i64, _i64, _p]),
     "flk_rope_embed": (_i, [_p, _i64, _i64, _i, _ip, _f, _p, _p]),
     "flk_lane_pair": (_i, [_p, _i64, _i, _p, _p, _p]),
     "flk_rope_lanes": (_i, [_p, _i64, _i64, _i, _ip, _f, _p, _p, _p]),

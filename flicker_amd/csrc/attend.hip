@@ -219,7 +219,7 @@ __device__ __forceinline__ void iteration(WaveState& w, const Ctx& c, int t, int
 __global__ __launch_bounds__(kThreads, 2) void attend_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, uint16_t* __restrict__ o, int length, int q_blocks,
-    int total_blocks) {
+    int total_blocks, int heads, int64_t o_batch_stride, int64_t o_head_stride, int64_t o_row_stride) {
   __shared__ __attribute__((aligned(1024))) uint8_t smem[kSmemBytes];
 
   // XCD-aware renumbering: hardware block id p runs on XCD p % 8; give each XCD a
@@ -338,7 +338,8 @@ __global__ __launch_bounds__(kThreads, 2) void attend_kernel(
   // Epilogue: l over both lane halves, O = bf16(acc / l), 4 d values per 8-byte store.
   const float l = w.lsum + __shfl_xor(w.lsum, 32);
   if (qi < length) {
-    uint16_t* orow = o + head_off + (int64_t)qi * kD;
+    const int b = bh / heads, h = bh - b * heads;
+    uint16_t* orow = o + b * o_batch_stride + h * o_head_stride + (int64_t)qi * o_row_stride;
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
 #pragma unroll
@@ -355,21 +356,41 @@ __global__ __launch_bounds__(kThreads, 2) void attend_kernel(
 
 }  // namespace
 
-extern "C" int flk_attend(const void* q, const void* k, const void* v, void* o, int batch,
-                          int heads, int length, int head_dim, void* stream) {
+namespace {
+
+int launch_attend(const void* q, const void* k, const void* v, void* o, int batch, int heads, int length,
+                  int head_dim, int64_t o_batch_stride, int64_t o_head_stride, int64_t o_row_stride,
+                  void* stream) {
   if (head_dim != kD) return FLK_E_UNSUPPORTED;
   if (batch < 0 || heads < 0 || length < 0) return FLK_E_INVALID;
   if (batch == 0 || heads == 0 || length == 0) return FLK_OK;
   if (!q || !k || !v || !o) return FLK_E_INVALID;
   if (!flk_host_aligned(q, 16) || !flk_host_aligned(k, 16) || !flk_host_aligned(v, 16) ||
-      !flk_host_aligned(o, 16))
+      !flk_host_aligned(o, 8) || o_batch_stride % 4 || o_head_stride % 4 || o_row_stride % 4)
     return FLK_E_ALIGN;
+  if (o_batch_stride < 0 || o_head_stride < 0 || o_row_stride < kD) return FLK_E_INVALID;
   const int64_t q_blocks = (length + kBM - 1) / kBM;
   const int64_t total = q_blocks * batch * heads;
   if (total > INT32_MAX) return FLK_E_INVALID;
   hipLaunchKernelGGL(attend_kernel, dim3((unsigned)total), dim3(kThreads), 0,
                      static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(q),
                      static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
-                     static_cast<uint16_t*>(o), length, (int)q_blocks, (int)total);
+                     static_cast<uint16_t*>(o), length, (int)q_blocks, (int)total, heads, o_batch_stride,
+                     o_head_stride, o_row_stride);
   return flk_launch_status();
+}
+
+}  // namespace
+
+extern "C" int flk_attend(const void* q, const void* k, const void* v, void* o, int batch,
+                          int heads, int length, int head_dim, void* stream) {
+  const int64_t row = kD, head = (int64_t)length * kD;
+  return launch_attend(q, k, v, o, batch, heads, length, head_dim, (int64_t)heads * head, head, row, stream);
+}
+
+extern "C" int flk_attend_to(const void* q, const void* k, const void* v, void* o, int batch, int heads,
+                             int length, int head_dim, int64_t o_batch_stride, int64_t o_head_stride,
+                             int64_t o_row_stride, void* stream) {
+  return launch_attend(q, k, v, o, batch, heads, length, head_dim, o_batch_stride, o_head_stride, o_row_stride,
+                       stream);
 }

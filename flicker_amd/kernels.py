@@ -7,6 +7,7 @@ tensors on an MI355X; every computation runs in the HIP kernels of libflicker_hi
   qk_prep                                         kernels.py:57-91  -> flk_qk_prep
   SCORE_TILES, EXP_LIMIT, logit_bound             kernels.py:94-101
   attend                                          kernels.py:105-145 -> flk_attend
+  attend_merged = merge_heads(attend(...))        + modules.py:63-65 -> flk_attend_to
 
 Beyond the reference, ``qk_prep`` takes optional ``out=(q, k, v)`` / ``out_offset`` so
 the text and image streams of a double block can be written straight into one
@@ -194,6 +195,39 @@ def attend(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, block: int | No
     elif out.shape != q.shape or out.dtype != torch.bfloat16 or not out.is_contiguous():
         raise ValueError("out must be a contiguous bf16 tensor shaped like q")
     _launch_attend(q, k, v, out)
+    return out
+
+
+def attend_merged(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
+                  out: torch.Tensor | None = None) -> torch.Tensor:
+    """``merge_heads(attend(q, k, v))`` (modules.py:63-65 after kernels.py:105-145) in one
+    kernel: the attention epilogue writes o[b, t, h*D:(h+1)*D] directly, so the transposing
+    copy of merge_heads disappears.  q, k, v (B, H, L, D) bf16 -> (B, L, H*D) bf16; ``out`` may
+    be a (B, L, H*D) view whose rows are strided (e.g. columns of a wider buffer)."""
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        if t.dim() != 4:
+            raise ValueError(f"{name} must be (B, H, L, D), got {tuple(t.shape)}")
+    if not (q.shape == k.shape == v.shape):
+        raise ValueError(f"q, k, v shapes differ: {tuple(q.shape)} {tuple(k.shape)} {tuple(v.shape)}")
+    batch, heads, length, dim = q.shape
+    if dim != HEAD_DIM:
+        raise ValueError(f"attend: head_dim {dim} unsupported (kernels are built for {HEAD_DIM})")
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        _on_gpu(name, t)
+        if t.dtype != torch.bfloat16:
+            raise TypeError(f"{name} must be bfloat16, got {t.dtype}")
+    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    if out is None:
+        out = torch.empty((batch, length, heads * dim), dtype=torch.bfloat16, device=q.device)
+    elif (out.shape != (batch, length, heads * dim) or out.dtype != torch.bfloat16 or out.stride(2) != 1
+          or out.stride(0) % 4 or out.stride(1) % 4 or out.data_ptr() % 8):
+        raise ValueError(f"out must be a bf16 ({batch}, {length}, {heads * dim}) view with contiguous, "
+                         "4-element aligned rows")
+    _on_gpu("out", out)
+    status = _lib.lib().flk_attend_to(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                                      batch, heads, length, dim, out.stride(0), dim, out.stride(1),
+                                      _lib.stream_of(q))
+    _lib.check(status, "flk_attend_to")
     return out
 
 

@@ -4,14 +4,15 @@ Reference: src/flicker/modules.py -- heads :56-60, merge_heads :63-65, qkv_prep 
 double_prepare_qkv :96-140 with double_block :156-158, single_prepare_qkv :180-191 with
 single_block :197-198.  These functions take the already-projected QKV activations
 (the linear/modulate parts of the blocks are outside this path) and return the
-merged attention output, in the same order and layout as the reference.
+merged attention output, in the same order and layout as the reference; the merge is
+done by the attention kernel's epilogue (kernels.attend_merged).
 """
 
 from __future__ import annotations
 
 import torch
 
-from .kernels import Freqs, _launch_qk_prep, attend, lane_pair
+from .kernels import Freqs, _launch_qk_prep, attend_merged, lane_pair
 
 
 def heads(qkv: torch.Tensor, num_heads: int):
@@ -57,7 +58,7 @@ def double_attention(txt_qkv, img_qkv, txt_scales, img_scales, freqs: Freqs, num
     qkv_prep(txt_qkv, *txt_scales, None, _slice(freqs, 0, num_txt), num_heads, out=joint, out_offset=0)
     qkv_prep(img_qkv, *img_scales, None, _slice(freqs, num_txt, num_txt + num_img), num_heads,
              out=joint, out_offset=num_txt)
-    attn = merge_heads(attend(*joint))
+    attn = attend_merged(*joint)   # merge_heads fused into the attention epilogue
     return attn[:, :num_txt], attn[:, num_txt:]
 
 
@@ -66,4 +67,4 @@ def single_attention(linear1_out, q_scale, k_scale, freqs: Freqs, num_heads: int
     consumed without a copy) -> qk prep -> attention -> merge; returns (attn, mlp)."""
     qkv, mlp = linear1_out[..., : 3 * hidden], linear1_out[..., 3 * hidden:]
     q, k, v = qkv_prep(qkv, q_scale, k_scale, None, freqs, num_heads)
-    return merge_heads(attend(q, k, v)), mlp
+    return attend_merged(q, k, v), mlp

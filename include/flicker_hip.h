@@ -65,6 +65,18 @@ int flk_attend(const void* q, const void* k, const void* v, void* o,
                int batch, int heads, int length, int head_dim, void* stream);
 
 /*
+ * flk_attend writing O through strides (elements): o[b, h, t, :] starts at
+ * o + b*o_batch_stride + h*o_head_stride + t*o_row_stride, the head_dim values contiguous.
+ * With (L*H*D, D, H*D) this is the token-major (batch, length, heads*head_dim) layout that
+ * merge_heads produces (src/flicker/modules.py:63-65), so attention writes the merged output
+ * directly instead of a (B, H, L, D) tensor plus a transposing copy (modules.py:157,198).
+ * Strides must be multiples of 4 elements, o 8-byte aligned, o_row_stride >= head_dim.
+ */
+int flk_attend_to(const void* q, const void* k, const void* v, void* o,
+                  int batch, int heads, int length, int head_dim,
+                  int64_t o_batch_stride, int64_t o_head_stride, int64_t o_row_stride, void* stream);
+
+/*
  * RoPE angle tables.  Replaces rope.embed_nd / rope.rope_freqs (src/flicker/rope.py:9-21):
  *   ids  (length, n_axes) float32 positions, row t at t*ids_row_stride floats
  *   axes_dim  host array of n_axes even ints (1 <= n_axes <= 8)

@@ -107,3 +107,22 @@ def test_attend_python_api_errors(device):
         kernels.attend(q, k, v, block=64)
     with pytest.raises(ValueError):
         kernels.attend(q, k, v, interpret=True)
+
+
+@pytest.mark.parametrize("batch,heads,length", [(1, 3, 100), (2, 2, 257), (1, 24, 1536)])
+def test_attend_merged_equals_merge_heads_of_attend(device, batch, heads, length):
+    """The token-major epilogue (flk_attend_to) writes exactly merge_heads(attend(q, k, v))
+    (modules.py:63-65): same kernel, different store address -> bit-identical."""
+    from flicker_amd import modules
+    q, k, v = (t.to(device) for t in prepped_case(batch, heads, length, seed=11 + length))
+    want = modules.merge_heads(kernels.attend(q, k, v, block=None if length % 128 == 0 else length))
+    got = kernels.attend_merged(q, k, v)
+    torch.cuda.synchronize()
+    assert got.shape == (batch, length, heads * D)
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+    # into the attention columns of a wider, row-strided buffer (e.g. a fused projection input)
+    wide = torch.full((batch, length, heads * D + 64), 7.0, dtype=torch.bfloat16, device=device)
+    kernels.attend_merged(q, k, v, out=wide[..., 32:32 + heads * D])
+    torch.cuda.synchronize()
+    assert torch.equal(wide[..., 32:32 + heads * D].view(torch.int16), want.view(torch.int16))
+    assert bool((wide[..., :32] == 7.0).all()) and bool((wide[..., 32 + heads * D:] == 7.0).all())

@@ -56,6 +56,12 @@ def test_attend_validation(lib):
     assert f(FAKE + 8, FAKE, FAKE, FAKE, 1, 24, 4608, 128, None) == _lib.FLK_E_ALIGN
     assert f(None, FAKE, FAKE, FAKE, 1, 24, 4608, 128, None) == _lib.FLK_E_INVALID
     assert f(FAKE, FAKE, FAKE, FAKE, 0, 24, 4608, 128, None) == _lib.FLK_OK       # empty: nothing launched
+    g = lib.flk_attend_to
+    hd = 24 * 128
+    assert g(FAKE, FAKE, FAKE, FAKE, 1, 24, 4608, 128, 4608 * hd, 128, hd + 2, None) == _lib.FLK_E_ALIGN
+    assert g(FAKE, FAKE, FAKE, FAKE + 4, 1, 24, 4608, 128, 4608 * hd, 128, hd, None) == _lib.FLK_E_ALIGN
+    assert g(FAKE, FAKE, FAKE, FAKE, 1, 24, 4608, 128, 4608 * hd, 128, 64, None) == _lib.FLK_E_INVALID
+    assert g(FAKE, FAKE, FAKE, FAKE, 1, 24, 4608, 64, 4608 * hd, 128, hd, None) == _lib.FLK_E_UNSUPPORTED
 
 
 def test_qk_prep_validation(lib):
