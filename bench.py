@@ -139,12 +139,47 @@ def w8a8_leg(args, timed, dev) -> dict:
     gemm_ms = timed(lambda i: w8a8.gemm(xq, a_scale, qw.wq_t, qw.w_scale, out=ys[i % 2]), args.steps)
     quant_ms = timed(lambda i: w8a8.quantize_act(x, qw.inv_smooth), args.steps)
     tops = p.gemm_ops() / (gemm_ms * 1e-3) / 1e12
+    # The projection feeding qk_prep: the GEMM + qk_prep pair, and the fused kernel whose
+    # epilogue does qk_prep (flk_w8a8_qk_prep), on the projection's tokens as one sequence.
+    from flicker_amd import kernels, rope
+    from flicker_amd.rope import sequence_ids
+    w_attn = workloads.WORKLOADS["klein_1024"]
+    heads = p.out_features // (3 * w_attn.head_dim)
+    qs, ks = (t.to(dev) for t in workloads.make_scales(w_attn))
+    n_txt = min(w_attn.num_txt, p.tokens)
+    side = int(round((p.tokens - n_txt) ** 0.5))
+    ids = sequence_ids(n_txt, side, (p.tokens - n_txt) // max(side, 1)) if p.tokens > n_txt else sequence_ids(n_txt, 0, 0)
+    freqs = rope.rope_lanes(ids, workloads.q_gain(w_attn), device=dev)
+    qkv_out = [tuple(torch.empty((1, heads, p.tokens, 128), dtype=torch.bfloat16, device=dev) for _ in range(3))
+               for _ in range(2)]
+    x3 = x.view(1, p.tokens, p.hidden)
+    lib = __import__("flicker_amd._lib", fromlist=["lib"])
+    stream = lib.stream_of(x)
+
+    def fused(i):
+        o = qkv_out[i % 2]
+        lib.check(lib.lib().flk_w8a8_qk_prep(
+            xq.data_ptr(), qw.wq_t.data_ptr(), a_scale.data_ptr(), qw.w_scale.data_ptr(), p.hidden,
+            freqs.cos.data_ptr(), freqs.sin.data_ptr(), freqs.cos.stride(0), qs.data_ptr(), ks.data_ptr(), 0,
+            freqs.q_gain, 1, p.tokens, heads, 128, o[0].data_ptr(), o[1].data_ptr(), o[2].data_ptr(),
+            p.tokens, 0, stream), "flk_w8a8_qk_prep")
+
+    def unfused(i):
+        y = ys[i % 2]
+        w8a8.gemm(xq, a_scale, qw.wq_t, qw.w_scale, out=y)
+        kernels.qk_prep(y.view(1, p.tokens, p.out_features), qs, ks, freqs, heads, out=qkv_out[i % 2])
+
+    fused_ms = timed(fused, args.steps)
+    unfused_ms = timed(unfused, args.steps)
+    del x3
     return {"workload": f"{p.name}: X ({p.tokens}, {p.hidden}) bf16 with {p.outlier_fraction:.0%} outlier "
                         f"channels x{p.outlier_gain:g}, W ({p.hidden}, {p.out_features}) ~ N(0, 0.02)",
             "roofline": {"bound": "mfma", "achieved": round(tops, 1), "peak": INT8_DENSE_PEAK_TOPS,
                          "unit": "TOP/s", "frac": round(tops / INT8_DENSE_PEAK_TOPS, 4), "kernel": "w8a8_gemm_kernel",
                          "ops_per_launch": p.gemm_ops(), "avg_launch_us": round(gemm_ms * 1e3, 2)},
             "quantize_act_us": round(quant_ms * 1e3, 2),
+            "gemm_then_qk_prep_us": round(unfused_ms * 1e3, 2),
+            "fused_gemm_qk_prep_us": round(fused_ms * 1e3, 2),
             "dtype": "int8 operands, int32 accumulate, bf16 out"}
 
 

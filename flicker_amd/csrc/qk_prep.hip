@@ -21,7 +21,7 @@
 //
 // The kernel is HBM-bound: per (b, t, h) it moves 3*256 bytes in and 3*256 out.
 
-#include "common.h"
+#include "qk_math.h"
 
 namespace {
 
@@ -61,69 +61,6 @@ __device__ __forceinline__ void store16(uint16_t* p, uint4 v) {
   }
 }
 
-template <bool kScaleF32>
-__device__ __forceinline__ void load_scale8(const void* scale, int lane, float out[8]) {
-  if constexpr (kScaleF32) {
-    const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(scale) + lane * 8);
-    float4 a = p[0], b = p[1];
-    out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
-    out[4] = b.x; out[5] = b.y; out[6] = b.z; out[7] = b.w;
-  } else {
-    uint4 w = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(scale) + lane * 8);
-    uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      out[2 * i] = flk::bf16_lo(ws[i]);
-      out[2 * i + 1] = flk::bf16_hi(ws[i]);
-    }
-  }
-}
-
-__device__ __forceinline__ void load_table8(const float* row, int lane, float out[8]) {
-  const float4* p = reinterpret_cast<const float4*>(row + lane * 8);
-  float4 a = p[0], b = p[1];
-  out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
-  out[4] = b.x; out[5] = b.y; out[6] = b.z; out[7] = b.w;
-}
-
-// RMSNorm * scale, RoPE rotation and optional gain on the 8 elements this lane holds.
-template <bool kScaleF32, bool kGain>
-__device__ __forceinline__ uint4 norm_rotate(uint4 raw, const float sc[8], const float c[8],
-                                             const float s[8], float gain) {
-#pragma clang fp contract(off)
-  const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
-  float x[8];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    x[2 * i] = flk::bf16_lo(w[i]);
-    x[2 * i + 1] = flk::bf16_hi(w[i]);
-  }
-  float ss = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) ss += x[i] * x[i];
-  ss = flk::row16_sum(ss);
-  const float ms = ss * (1.0f / kHeadDim);
-  const float inv = 1.0f / sqrtf(ms + 1e-6f);
-  float y[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const float n = flk::round_bf16(x[i] * inv);
-    y[i] = kScaleF32 ? n * sc[i] : flk::round_bf16(n * sc[i]);
-  }
-  float r[8];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    r[2 * j] = c[2 * j] * y[2 * j] + s[2 * j] * y[2 * j + 1];
-    r[2 * j + 1] = c[2 * j + 1] * y[2 * j + 1] + s[2 * j + 1] * y[2 * j];
-  }
-  if constexpr (kGain) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) r[i] = gain * r[i];
-  }
-  return make_uint4(flk::pack_bf16x2(r[0], r[1]), flk::pack_bf16x2(r[2], r[3]),
-                    flk::pack_bf16x2(r[4], r[5]), flk::pack_bf16x2(r[6], r[7]));
-}
-
 template <bool kScaleF32, bool kGain, int kHeads>
 __global__ __launch_bounds__(kThreads) void qk_prep_kernel(
     const uint16_t* __restrict__ qkv, int64_t batch_stride, int64_t row_stride,
@@ -146,17 +83,17 @@ __global__ __launch_bounds__(kThreads) void qk_prep_kernel(
     rv[i] = load16(row + (int64_t)(2 * num_heads + h0 + i) * kHeadDim);
   }
   float c[8], s[8], qs[8], ks[8];
-  load_table8(cos_t + (int64_t)t * table_stride, lane, c);
-  load_table8(sin_t + (int64_t)t * table_stride, lane, s);
-  load_scale8<kScaleF32>(q_scale, lane, qs);
-  load_scale8<kScaleF32>(k_scale, lane, ks);
+  flk::load_table8(cos_t + (int64_t)t * table_stride, lane, c);
+  flk::load_table8(sin_t + (int64_t)t * table_stride, lane, s);
+  flk::load_scale8<kScaleF32>(q_scale, lane, qs);
+  flk::load_scale8<kScaleF32>(k_scale, lane, ks);
 
 #pragma unroll
   for (int i = 0; i < kHeads; ++i) {
     const int64_t o =
         (((int64_t)b * num_heads + h0 + i) * out_length + out_offset + t) * kHeadDim + lane * 8;
-    store16(q_out + o, norm_rotate<kScaleF32, kGain>(rq[i], qs, c, s, q_gain));
-    store16(k_out + o, norm_rotate<kScaleF32, false>(rk[i], ks, c, s, 1.0f));
+    store16(q_out + o, flk::norm_rotate<kScaleF32, kGain>(rq[i], qs, c, s, q_gain));
+    store16(k_out + o, flk::norm_rotate<kScaleF32, false>(rk[i], ks, c, s, 1.0f));
     store16(v_out + o, rv[i]);
   }
 }

@@ -32,7 +32,7 @@
 // on distinct banks.  Blocks are renumbered so consecutive output tiles share an XCD
 // (and its L2), and grouped so that 4 token tiles sweep the channel tiles together.
 
-#include "common.h"
+#include "qk_math.h"
 
 namespace {
 
@@ -298,13 +298,30 @@ __device__ __forceinline__ void gemm_step(i32x16 (&acc)[4][4], const i32x4 (&cur
   }
 }
 
+// The fused epilogue's qk_prep parameters (see flk_w8a8_qk_prep): output row m of the
+// projection is token t = m % length of batch b = m / length, and its 128-channel head
+// groups are q heads 0..H-1, then k heads, then v heads.
+struct QkEpilogue {
+  const float* cos;
+  const float* sin;
+  int64_t table_stride;
+  const void* q_scale;
+  const void* k_scale;
+  float q_gain;
+  int length, heads;
+  uint16_t* out[3];
+  int64_t out_length, out_offset;
+};
+
 // kAcc: also write the exact int32 products (a test and debugging path; its accumulator
 // copies cost registers, so the production instantiation leaves it out).
-template <bool kAcc>
+// kQk: instead of Y, run qk_prep on each finished bf16 head row (kScaleF32: float32 norm
+// scales) and write head-major q, k, v.
+template <bool kAcc, bool kQk = false, bool kScaleF32 = false>
 __global__ __launch_bounds__(kGThreads, 1) void w8a8_gemm_kernel(
     const int8_t* __restrict__ xq, const int8_t* __restrict__ wqt, const float* __restrict__ a_scale,
     const float* __restrict__ w_scale, uint16_t* __restrict__ y, int64_t y_stride,
-    int32_t* __restrict__ acc_out, int M, int K, int N, int tiles_m, int tiles_n) {
+    int32_t* __restrict__ acc_out, int M, int K, int N, int tiles_m, int tiles_n, QkEpilogue qe) {
   __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * kGStage];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -451,6 +468,37 @@ __global__ __launch_bounds__(kGThreads, 1) void w8a8_gemm_kernel(
   // Each wave reads back only what it wrote itself: its LDS writes complete in order before
   // its reads (the compiler waits on lgkmcnt), so no barrier is needed here.
   const int n_lane = n0 + wn * 128 + (lane & 15) * 8;
+  if constexpr (kQk) {
+    // The wave's 128 channels are one head of the q|k|v thirds (N = 3 H 128, tiles 128-aligned);
+    // each 16-lane row of a read-back is one token's finished bf16 head row -- the input of
+    // qk_prep, rounded exactly as the unfused path stores it in Y.
+    const int head_g = (n0 + wn * 128) / flk::kQkHeadDim;
+    if (n0 + wn * 128 >= N) return;
+    const int sec = head_g / qe.heads, h = head_g - sec * qe.heads;
+    const int l16 = lane & 15;
+    float sc[8];
+    if (sec < 2) flk::load_scale8<kScaleF32>(sec == 0 ? qe.q_scale : qe.k_scale, l16, sc);
+    uint16_t* const out = qe.out[sec];
+#pragma unroll 4
+    for (int it = 0; it < 32; ++it) {
+      const int ml = it * 4 + (lane >> 4);
+      const uint4 v = *reinterpret_cast<const uint4*>(out_lds + ml * 256 + ((l16 ^ (ml & 15)) * 16));
+      const int m = m0 + wm * 128 + ml;
+      if (m >= M) continue;   // uniform over the 16-lane row, so the DPP rows stay whole
+      const int b = m / qe.length, t = m - b * qe.length;
+      uint4 r = v;
+      if (sec < 2) {
+        float c[8], s[8];
+        flk::load_table8(qe.cos + (int64_t)t * qe.table_stride, l16, c);
+        flk::load_table8(qe.sin + (int64_t)t * qe.table_stride, l16, s);
+        r = sec == 0 ? flk::norm_rotate<kScaleF32, true>(v, sc, c, s, qe.q_gain)
+                     : flk::norm_rotate<kScaleF32, false>(v, sc, c, s, 1.0f);
+      }
+      const int64_t o = (((int64_t)b * qe.heads + h) * qe.out_length + qe.out_offset + t) * flk::kQkHeadDim + l16 * 8;
+      *reinterpret_cast<uint4*>(out + o) = r;
+    }
+    return;
+  }
   const bool wide = (y_stride & 7) == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0;   // 16-byte rows
 #pragma unroll 8
   for (int it = 0; it < 32; ++it) {
@@ -567,10 +615,49 @@ extern "C" int flk_w8a8_gemm(const int8_t* xq, const int8_t* wq_t, const float* 
   if (acc_or_null)
     hipLaunchKernelGGL(w8a8_gemm_kernel<true>, dim3((unsigned)blocks), dim3(kGThreads), 0, as_stream(stream), xq,
                        wq_t, a_scale, w_scale, static_cast<uint16_t*>(y), y_row_stride, acc_or_null, m, k, n, tiles_m,
-                       tiles_n);
+                       tiles_n, QkEpilogue{});
   else
     hipLaunchKernelGGL(w8a8_gemm_kernel<false>, dim3((unsigned)blocks), dim3(kGThreads), 0, as_stream(stream), xq,
                        wq_t, a_scale, w_scale, static_cast<uint16_t*>(y), y_row_stride, nullptr, m, k, n, tiles_m,
-                       tiles_n);
+                       tiles_n, QkEpilogue{});
+  return flk_launch_status();
+}
+
+extern "C" int flk_w8a8_qk_prep(const int8_t* xq, const int8_t* wq_t, const float* a_scale, const float* w_scale,
+                                int k, const float* cos, const float* sin, int64_t table_row_stride,
+                                const void* q_scale, const void* k_scale, int scale_is_f32, float q_gain, int batch,
+                                int length, int num_heads, int head_dim, void* q_out, void* k_out, void* v_out,
+                                int64_t out_length, int64_t out_offset, void* stream) {
+  if (head_dim != flk::kQkHeadDim) return FLK_E_UNSUPPORTED;
+  if (batch < 0 || length < 0 || num_heads <= 0 || k < 0 || out_offset < 0 || out_offset + length > out_length)
+    return FLK_E_INVALID;
+  if (batch == 0 || length == 0) return FLK_OK;
+  if (!xq || !wq_t || !a_scale || !w_scale || !cos || !sin || !q_scale || !k_scale || !q_out || !k_out ||
+      !v_out || k == 0 || table_row_stride < head_dim)
+    return FLK_E_INVALID;
+  if (k % 128) return FLK_E_UNSUPPORTED;
+  if ((int64_t)k * 127 * 127 > INT32_MAX) return FLK_E_UNSUPPORTED;
+  const int64_t m64 = (int64_t)batch * length, n = 3LL * num_heads * head_dim;
+  if (m64 > INT32_MAX || n > INT32_MAX) return FLK_E_INVALID;
+  if (!flk_host_aligned(xq, 16) || !flk_host_aligned(wq_t, 16) || !flk_host_aligned(w_scale, 16) ||
+      !flk_host_aligned(a_scale, 4) || !flk_host_aligned(cos, 16) || !flk_host_aligned(sin, 16) ||
+      table_row_stride % 4 || !flk_host_aligned(q_scale, 16) || !flk_host_aligned(k_scale, 16) ||
+      !flk_host_aligned(q_out, 16) || !flk_host_aligned(k_out, 16) || !flk_host_aligned(v_out, 16))
+    return FLK_E_ALIGN;
+  const int m = (int)m64;
+  const int tiles_m = (m + kGT - 1) / kGT, tiles_n = (int)((n + kGT - 1) / kGT);
+  const int64_t blocks = (int64_t)tiles_m * tiles_n;
+  if (blocks > INT32_MAX) return FLK_E_INVALID;
+  QkEpilogue qe{cos, sin, table_row_stride, q_scale, k_scale, q_gain, length, num_heads,
+                {static_cast<uint16_t*>(q_out), static_cast<uint16_t*>(k_out), static_cast<uint16_t*>(v_out)},
+                out_length, out_offset};
+  if (scale_is_f32)
+    hipLaunchKernelGGL((w8a8_gemm_kernel<false, true, true>), dim3((unsigned)blocks), dim3(kGThreads), 0,
+                       as_stream(stream), xq, wq_t, a_scale, w_scale, nullptr, 0, nullptr, m, k, (int)n, tiles_m,
+                       tiles_n, qe);
+  else
+    hipLaunchKernelGGL((w8a8_gemm_kernel<false, true, false>), dim3((unsigned)blocks), dim3(kGThreads), 0,
+                       as_stream(stream), xq, wq_t, a_scale, w_scale, nullptr, 0, nullptr, m, k, (int)n, tiles_m,
+                       tiles_n, qe);
   return flk_launch_status();
 }

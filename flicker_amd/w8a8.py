@@ -166,3 +166,53 @@ def linear(x: torch.Tensor, qw: QuantizedLinear, *, out: torch.Tensor | None = N
     xq, a_scale = quantize_act(x, qw.inv_smooth)
     y = gemm(xq, a_scale, qw.wq_t, qw.w_scale, out=None if out is None else out.view(-1, qw.out_features))
     return y.reshape(*lead, qw.out_features) if out is None else out
+
+
+def qk_prep(x: torch.Tensor, qw: QuantizedLinear, q_scale: torch.Tensor, k_scale: torch.Tensor, freqs,
+            num_heads: int, *, out=None, out_offset: int = 0):
+    """``kernels.qk_prep(linear(x, qw), q_scale, k_scale, freqs, num_heads)`` in two launches
+    instead of three: the activation quantisation, then one int8 GEMM whose epilogue applies
+    QK-RMSNorm + RoPE (+ q_gain) to each finished head row and writes head-major q, k, v
+    (kernels.py:57-91 after nn.py:13-14); the projected activation never reaches memory.
+    Bit-identical to the unfused pair.  x (B, L, K) bf16 -> q, k, v (B, H, L, 128) bf16."""
+    from .kernels import HEAD_DIM, Freqs
+
+    if x.dim() != 3:
+        raise ValueError(f"x must be (B, L, K), got {tuple(x.shape)}")
+    batch, length, k = x.shape
+    if qw.out_features != 3 * num_heads * HEAD_DIM:
+        raise ValueError(f"projection has {qw.out_features} outputs, not 3 * {num_heads} * {HEAD_DIM}")
+    cos, sin, q_gain = Freqs(*freqs)
+    for name, t in (("freqs.cos", cos), ("freqs.sin", sin), ("q_scale", q_scale), ("k_scale", k_scale)):
+        _on_gpu(name, t)
+    if cos.shape != (length, HEAD_DIM) or sin.shape != (length, HEAD_DIM) or cos.dtype != torch.float32 \
+            or sin.dtype != torch.float32:
+        raise ValueError(f"freqs tables must be float32 ({length}, {HEAD_DIM})")
+    cos, sin = cos.contiguous(), sin.contiguous()
+    if q_scale.dtype != k_scale.dtype or q_scale.dtype not in (torch.bfloat16, torch.float32) \
+            or q_scale.numel() != HEAD_DIM or k_scale.numel() != HEAD_DIM:
+        raise ValueError(f"q_scale / k_scale must be {HEAD_DIM} bfloat16 or float32 values of one dtype")
+    q_scale, k_scale = q_scale.reshape(-1).contiguous(), k_scale.reshape(-1).contiguous()
+    xq, a_scale = quantize_act(x, qw.inv_smooth)
+    if out is None:
+        if out_offset:
+            raise ValueError("out_offset needs out=(q, k, v)")
+        out = tuple(torch.empty((batch, num_heads, length, HEAD_DIM), dtype=torch.bfloat16, device=x.device)
+                    for _ in range(3))
+        out_length = length
+    else:
+        out = tuple(out)
+        out_length = out[0].shape[2]
+        for t in out:
+            if (t.dtype != torch.bfloat16 or t.shape != (batch, num_heads, out_length, HEAD_DIM)
+                    or not t.is_contiguous()):
+                raise ValueError("out tensors must be contiguous bf16 (B, H, L_out, D) of one shape")
+        if out_offset < 0 or out_offset + length > out_length:
+            raise ValueError(f"out_offset {out_offset} + L {length} exceeds the output length {out_length}")
+    _lib.check(_lib.lib().flk_w8a8_qk_prep(
+        xq.data_ptr(), qw.wq_t.data_ptr(), a_scale.data_ptr(), qw.w_scale.data_ptr(), k, cos.data_ptr(),
+        sin.data_ptr(), cos.stride(0), q_scale.data_ptr(), k_scale.data_ptr(),
+        int(q_scale.dtype == torch.float32), float(q_gain), batch, length, num_heads, HEAD_DIM,
+        out[0].data_ptr(), out[1].data_ptr(), out[2].data_ptr(), out_length, out_offset,
+        _lib.stream_of(x)), "flk_w8a8_qk_prep")
+    return out

@@ -143,6 +143,22 @@ int flk_w8a8_gemm(const int8_t* xq, const int8_t* wq_t, const float* a_scale, co
                   int m, int k, int n, void* y, int64_t y_row_stride, int32_t* acc_or_null,
                   void* stream);
 
+/* int8 projection and qk_prep in one kernel: qk_prep(bf16(rescaled xq . wq_t^T)) with the
+ * GEMM's epilogue doing the RMSNorm + RoPE of each finished head row, so the projected
+ * activation Y never goes to memory.  Replaces the pair linear(x, w) (src/flicker/nn.py:13-14
+ * at modules.py:128,132,186) -> qk_prep (src/flicker/kernels.py:57-91), with the int8
+ * projection above; bit-identical to flk_w8a8_gemm followed by flk_qk_prep.
+ *   xq (batch*length, k) int8, wq_t (3*num_heads*head_dim, k) int8, a_scale / w_scale as for
+ *   flk_w8a8_gemm; cos, sin, q_scale, k_scale, scale_is_f32, q_gain, q_out/k_out/v_out,
+ *   out_length and out_offset as for flk_qk_prep (output row m = b*length + t).
+ * k % 128 == 0, head_dim must be 128. */
+int flk_w8a8_qk_prep(const int8_t* xq, const int8_t* wq_t, const float* a_scale, const float* w_scale, int k,
+                     const float* cos, const float* sin, int64_t table_row_stride,
+                     const void* q_scale, const void* k_scale, int scale_is_f32, float q_gain,
+                     int batch, int length, int num_heads, int head_dim,
+                     void* q_out, void* k_out, void* v_out, int64_t out_length, int64_t out_offset,
+                     void* stream);
+
 #ifdef __cplusplus
 }
 #endif

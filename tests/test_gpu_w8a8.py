@@ -204,6 +204,54 @@ def test_quantisation_error_against_bf16_projection(device):
     assert rel < 0.03, rel
 
 
+def _fused_case(device, batch, length, heads, k, scale_dtype, gain, seed):
+    from flicker_amd import kernels, rope
+    from oracle import path as P
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(batch, length, k, generator=g)
+    x[..., 5] *= 20.0                                                # an outlier channel
+    w = 0.02 * torch.randn(k, 3 * heads * 128, generator=g)
+    qs = (1 + 0.05 * torch.randn(128, generator=g)).to(scale_dtype)
+    ks = (1 + 0.05 * torch.randn(128, generator=g)).to(scale_dtype)
+    x, w = x.to(torch.bfloat16).to(device), w.to(torch.bfloat16).to(device)
+    qw = w8a8.quantize_linear(w, w8a8.absmax_cols(x))
+    ids = P.sequence_ids(min(length, 16), 1, max(length - 16, 0)) if length > 16 else P.sequence_ids(length, 0, 0)
+    freqs = rope.rope_lanes(ids, gain, device=device)
+    qs, ks = qs.to(device), ks.to(device)
+    return x, qw, qs, ks, freqs, kernels
+
+
+@pytest.mark.parametrize("batch,length,heads,k,scale_dtype,gain", [
+    (1, 4608, 24, 3072, torch.bfloat16, 128 ** -0.5),   # the 1024^2 Klein projection feeding qk_prep
+    (2, 257, 2, 256, torch.float32, 1.0),               # ragged token tiles, f32 scales, no gain
+    (1, 40, 3, 128, torch.bfloat16, 0.3),
+])
+def test_fused_projection_qk_prep_bit_exact(device, batch, length, heads, k, scale_dtype, gain):
+    """flk_w8a8_qk_prep == flk_qk_prep(flk_w8a8_gemm(...)) bit for bit: the epilogue applies
+    the same row arithmetic (one shared implementation) to the same bf16 projected values."""
+    x, qw, qs, ks, freqs, kernels = _fused_case(device, batch, length, heads, k, scale_dtype, gain, seed=length)
+    y = w8a8.linear(x, qw)
+    want = kernels.qk_prep(y, qs, ks, freqs, heads, rows=length)
+    got = w8a8.qk_prep(x, qw, qs, ks, freqs, heads)
+    torch.cuda.synchronize()
+    for name, a, b in zip("qkv", got, want):
+        assert a.shape == b.shape == (batch, heads, length, 128)
+        bad = int((a.view(torch.int16) != b.view(torch.int16)).sum())
+        assert bad == 0, f"{name}: {bad} of {a.numel()} elements differ"
+
+
+def test_fused_projection_writes_at_sequence_offset(device):
+    """out/out_offset place the stream inside a joint text|image buffer, as for qk_prep."""
+    x, qw, qs, ks, freqs, kernels = _fused_case(device, 1, 64, 2, 128, torch.bfloat16, 0.5, seed=3)
+    joint = tuple(torch.full((1, 2, 100, 128), 3.0, dtype=torch.bfloat16, device=device) for _ in range(3))
+    w8a8.qk_prep(x, qw, qs, ks, freqs, 2, out=joint, out_offset=20)
+    want = kernels.qk_prep(w8a8.linear(x, qw), qs, ks, freqs, 2)
+    torch.cuda.synchronize()
+    for a, b in zip(joint, want):
+        assert torch.equal(a[:, :, 20:84].view(torch.int16), b.view(torch.int16))
+        assert bool((a[:, :, :20] == 3.0).all()) and bool((a[:, :, 84:] == 3.0).all())
+
+
 def test_errors(device):
     x = torch.zeros((4, 100), dtype=torch.bfloat16, device=device)
     with pytest.raises(Exception, match="status -3"):        # k % 8
