@@ -20,12 +20,12 @@
 // WqT (N, K) int8, so both GEMM operands are K-contiguous rows; Y (M, N) bf16 with a
 // row stride; optional acc (M, N) int32.
 //
-// GEMM.  A block of 4 waves owns a 256 (n) x 256 (m) output tile and computes it
-// transposed, Y^T = WqT . Xq^T, with v_mfma_i32_32x32x32_i8: A operand = 32 WqT rows x
-// 32 k bytes, B operand = 32 Xq rows x 32 k bytes, both one ds_read_b128 per lane.  In
-// the 32x32 accumulator a lane owns one token and 4 x 4 consecutive output channels, so
-// the epilogue stores 4 bf16 (8 bytes) per register group.  Each wave holds a 128 x 128
-// sub-tile: 16 accumulators of 16 int32 (256 registers), 8 operand reads per 16 MFMAs.
+// GEMM.  A block of 8 waves (two per SIMD) owns a 256 (n) x 256 (m) output tile and
+// computes it transposed, Y^T = WqT . Xq^T, with v_mfma_i32_32x32x32_i8: A operand = 32 WqT
+// rows x 32 k bytes, B operand = 32 Xq rows x 32 k bytes, both one ds_read_b128 per lane.
+// In the 32x32 accumulator a lane owns one token and 4 x 4 consecutive output channels, so
+// the epilogue stores 4 bf16 (8 bytes) per register group.  Each wave holds a 128 (n) x 64
+// (m) sub-tile: 8 accumulators of 16 int32 (128 registers), 6 operand reads per 8 MFMAs.
 // k advances in 64-byte stages through a 4-stage LDS ring filled by
 // global_load_lds_dwordx4 (no registers); stage rows are 64 bytes = 4 chunks of 16 B
 // stored at chunk ^ ((row >> 1) & 3), which keeps each 8-lane phase of an operand read
@@ -257,8 +257,13 @@ constexpr int kGT = 256;                 // tile edge: tokens and output channel
 constexpr int kGK = 128;                 // k bytes per stage: one full 128-byte line per row
 constexpr int kGHalf = kGT * kGK;        // one operand's stage: 32 KiB
 constexpr int kGStage = 2 * kGHalf;      // WqT rows, then Xq rows; two stages fill 128 KiB
-constexpr int kGThreads = 256;
-constexpr int kGCopies = 8;              // copy instructions per operand per wave and stage
+constexpr int kGWaves = 8;               // two waves per SIMD
+constexpr int kGThreads = kGWaves * 64;
+constexpr int kGWaveN = 128;             // a wave's output channels (4 fragments of 32)
+constexpr int kGWaveM = 64;              // a wave's tokens (2 fragments of 32)
+constexpr int kGMT = kGWaveM / 32;
+constexpr int kGCopies = kGT / kGWaves / 8;   // copy instructions per operand per wave and stage (4)
+constexpr int kGFrags = 4 + kGMT;             // operand fragments per k step: 4 WqT + 2 Xq
 #ifndef FLK_GEMM_GROUP
 #define FLK_GEMM_GROUP 4
 #endif
@@ -271,28 +276,29 @@ constexpr int kXcds = 8;
 // distinct (row parity, slot) pairs, so neither 8-lane nor 16-lane read phases collide.
 __device__ __forceinline__ int gswz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
 
-// One 32-byte k step of the wave's 128 x 128 sub-tile: 16 MFMAs on the fragments in `cur`,
+__device__ __forceinline__ const uint8_t* frag_base(const uint8_t* stage, int i, int wn, int wm) {
+  return i < 4 ? stage + (wn * kGWaveN + i * 32) * kGK : stage + kGHalf + (wm * kGWaveM + (i - 4) * 32) * kGK;
+}
+
+// One 32-byte k step of the wave's 128 x 64 sub-tile: 8 MFMAs on the fragments in `cur`,
 // interleaved with the reads of the next step's fragments into `nxt` and, in the step that
 // follows the barrier, the copies that refill the stage just consumed.
 template <bool kCopy>
-__device__ __forceinline__ void gemm_step(i32x16 (&acc)[4][4], const i32x4 (&cur)[8], i32x4 (&nxt)[8],
-                                          const uint8_t* src, int off, int wn, int wm, const int8_t* abase,
-                                          const int8_t* bbase, const uint32_t (&aoff)[kGCopies],
-                                          const uint32_t (&boff)[kGCopies], uint8_t* dst) {
+__device__ __forceinline__ void gemm_step(i32x16 (&acc)[4][kGMT], const i32x4 (&cur)[kGFrags],
+                                          i32x4 (&nxt)[kGFrags], const uint8_t* src, int off, int wn, int wm,
+                                          const int8_t* abase, const int8_t* bbase,
+                                          const uint32_t (&aoff)[kGCopies], const uint32_t (&boff)[kGCopies],
+                                          uint8_t* dst) {
 #pragma unroll
   for (int nt = 0; nt < 4; ++nt) {
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int i = 2 * nt + j;
-      const uint8_t* base = i < 4 ? src + (wn * 128 + i * 32) * kGK : src + kGHalf + (wm * 128 + (i - 4) * 32) * kGK;
-      nxt[i] = *reinterpret_cast<const i32x4*>(base + off);
-      if constexpr (kCopy) {
-        flk::dma16_at(abase, aoff[i], dst + i * 8 * kGK);
-        flk::dma16_at(bbase, boff[i], dst + kGHalf + i * 8 * kGK);
-      }
+    nxt[nt] = *reinterpret_cast<const i32x4*>(frag_base(src, nt, wn, wm) + off);
+    if (nt < kGMT) nxt[4 + nt] = *reinterpret_cast<const i32x4*>(frag_base(src, 4 + nt, wn, wm) + off);
+    if constexpr (kCopy) {
+      flk::dma16_at(abase, aoff[nt], dst + nt * 8 * kGK);
+      flk::dma16_at(bbase, boff[nt], dst + kGHalf + nt * 8 * kGK);
     }
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
+    for (int mt = 0; mt < kGMT; ++mt)
       acc[nt][mt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(cur[nt], cur[4 + mt], acc[nt][mt], 0, 0, 0);
     __builtin_amdgcn_sched_barrier(0);
   }
@@ -313,12 +319,11 @@ struct QkEpilogue {
   int64_t out_length, out_offset;
 };
 
-// kAcc: also write the exact int32 products (a test and debugging path; its accumulator
-// copies cost registers, so the production instantiation leaves it out).
+// kAcc: also write the exact int32 products (a test and debugging path).
 // kQk: instead of Y, run qk_prep on each finished bf16 head row (kScaleF32: float32 norm
 // scales) and write head-major q, k, v.
 template <bool kAcc, bool kQk = false, bool kScaleF32 = false>
-__global__ __launch_bounds__(kGThreads, 1) void w8a8_gemm_kernel(
+__global__ __launch_bounds__(kGThreads, 2) void w8a8_gemm_kernel(
     const int8_t* __restrict__ xq, const int8_t* __restrict__ wqt, const float* __restrict__ a_scale,
     const float* __restrict__ w_scale, uint16_t* __restrict__ y, int64_t y_stride,
     int32_t* __restrict__ acc_out, int M, int K, int N, int tiles_m, int tiles_n, QkEpilogue qe) {
@@ -341,7 +346,7 @@ __global__ __launch_bounds__(kGThreads, 1) void w8a8_gemm_kernel(
   const int m0 = (first_m + in_group % gm) * kGT;
   const int n0 = (in_group / gm) * kGT;
 
-  // Copy sources: this wave fills rows wave*64 .. +63 of both operands, 8 rows (64 lanes x
+  // Copy sources: this wave fills rows wave*32 .. +31 of both operands, 8 rows (64 lanes x
   // 16 B) per instruction; lane i lands at row i/8, slot i%8, and fetches chunk slot^gswz.
   // Rows past the matrix edge repeat the last row (their results are never stored).  The
   // tile's first row (plus the stage's k offset) is a scalar base; lanes add 32-bit offsets.
@@ -350,38 +355,25 @@ __global__ __launch_bounds__(kGThreads, 1) void w8a8_gemm_kernel(
   uint32_t aoff[kGCopies], boff[kGCopies];
 #pragma unroll
   for (int i = 0; i < kGCopies; ++i) {
-    const int row = wave * 64 + i * 8 + (lane >> 3);
+    const int row = wave * (kGT / kGWaves) + i * 8 + (lane >> 3);
     const uint32_t chunk = (uint32_t)(((lane & 7) ^ gswz(row)) * 16);
     aoff[i] = (uint32_t)min(row, N - 1 - n0) * (uint32_t)K + chunk;
     boff[i] = (uint32_t)min(row, M - 1 - m0) * (uint32_t)K + chunk;
   }
-  uint8_t* const wave_lds = smem + wave * 64 * kGK;   // this wave's copy rows in stage 0
+  uint8_t* const wave_lds = smem + wave * (kGT / kGWaves) * kGK;   // this wave's copy rows in stage 0
 
   const int KT = K / kGK;
-  const int wn = wave >> 1, wm = wave & 1;
+  const int wn = wave >> 2, wm = wave & 3;     // 2 (channels) x 4 (tokens) waves
   const int l32 = lane & 31, half = lane >> 5;
   int off[4];
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) off[ks] = l32 * kGK + (((2 * ks + half) ^ gswz(l32)) * 16);
 
-  // The epilogue's scales, fetched now so their latency hides behind the main loop: a_t of
-  // the lane's 4 tokens and w_o of its 4 x 4 groups of 4 channels (clamped at the edges;
-  // clamped values are never stored).
-  float am[4];
-#pragma unroll
-  for (int mt = 0; mt < 4; ++mt) am[mt] = a_scale[min(m0 + wm * 128 + mt * 32 + l32, M - 1)];
-  f32x4 ws[4][4];
-#pragma unroll
-  for (int nt = 0; nt < 4; ++nt)
-#pragma unroll
-    for (int g = 0; g < 4; ++g)
-      ws[nt][g] = *reinterpret_cast<const f32x4*>(w_scale + min(n0 + wn * 128 + nt * 32 + g * 8 + half * 4, N - 4));
-
-  i32x16 acc[4][4];
+  i32x16 acc[4][kGMT];
 #pragma unroll
   for (int a = 0; a < 4; ++a)
 #pragma unroll
-    for (int b = 0; b < 4; ++b) acc[a][b] = i32x16{};
+    for (int b = 0; b < kGMT; ++b) acc[a][b] = i32x16{};
 
   // Two stages.  Iteration kt multiplies k steps 0..2 of stage kt while reading the next
   // step's fragments; then, once stage kt+1 has landed everywhere and every wave has read
@@ -401,12 +393,9 @@ __global__ __launch_bounds__(kGThreads, 1) void w8a8_gemm_kernel(
   }
   asm volatile("s_waitcnt vmcnt(%0)" :: "n"(2 * kGCopies) : "memory");   // stage 0 landed
   __syncthreads();
-  i32x4 ra[8], rb[8];
+  i32x4 ra[kGFrags], rb[kGFrags];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const uint8_t* base = i < 4 ? smem + (wn * 128 + i * 32) * kGK : smem + kGHalf + (wm * 128 + (i - 4) * 32) * kGK;
-    ra[i] = *reinterpret_cast<const i32x4*>(base + off[0]);
-  }
+  for (int i = 0; i < kGFrags; ++i) ra[i] = *reinterpret_cast<const i32x4*>(frag_base(smem, i, wn, wm) + off[0]);
 
   for (int kt = 0; kt < KT; ++kt) {
     const int cur = (kt & 1) * kGStage, nxt = ((kt + 1) & 1) * kGStage;
@@ -427,10 +416,10 @@ __global__ __launch_bounds__(kGThreads, 1) void w8a8_gemm_kernel(
     for (int nt = 0; nt < 4; ++nt)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const int n = n0 + wn * 128 + nt * 32 + g * 8 + half * 4;
+        const int n = n0 + wn * kGWaveN + nt * 32 + g * 8 + half * 4;
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-          const int m = m0 + wm * 128 + mt * 32 + l32;
+        for (int mt = 0; mt < kGMT; ++mt) {
+          const int m = m0 + wm * kGWaveM + mt * 32 + l32;
           if (n < N && m < M)
             *reinterpret_cast<i32x4*>(acc_out + (int64_t)m * N + n) =
                 i32x4{acc[nt][mt][4 * g], acc[nt][mt][4 * g + 1], acc[nt][mt][4 * g + 2], acc[nt][mt][4 * g + 3]};
@@ -439,20 +428,24 @@ __global__ __launch_bounds__(kGThreads, 1) void w8a8_gemm_kernel(
   }
 
   // Epilogue.  The lane owns token m = mt*32 + l32 and, per register group g, channels
-  // n = nt*32 + 8g + 4*half .. +3 of the wave's 128 x 128 sub-tile.  Rescaled bf16 values go
-  // to this wave's 32 KiB of the (now idle) LDS as [m][n] rows of 256 B whose 16-byte chunks
+  // n = nt*32 + 8g + 4*half .. +3 of the wave's 128 x 64 sub-tile.  Rescaled bf16 values go
+  // to this wave's 16 KiB of the (now idle) LDS as [m][n] rows of 256 B whose 16-byte chunks
   // are XOR-swizzled by m & 15; then the wave reads back 4 rows per instruction (16 lanes x
   // 16 B per row) and writes each row's 256 contiguous bytes with 16-byte stores.
+  float am[kGMT];
+#pragma unroll
+  for (int mt = 0; mt < kGMT; ++mt) am[mt] = a_scale[min(m0 + wm * kGWaveM + mt * 32 + l32, M - 1)];
   __syncthreads();   // every wave is done reading the operand stages
-  uint8_t* const out_lds = smem + wave * (128 * 256);
+  uint8_t* const out_lds = smem + wave * (kGWaveM * 256);
 #pragma unroll
   for (int nt = 0; nt < 4; ++nt) {
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
+      // w_o of the lane's 4 channels (clamped at the edge; clamped values are never stored)
+      const f32x4 w4 = *reinterpret_cast<const f32x4*>(w_scale + min(n0 + wn * kGWaveN + nt * 32 + g * 8 + half * 4, N - 4));
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
+      for (int mt = 0; mt < kGMT; ++mt) {
         const int ml = mt * 32 + l32;
-        const f32x4 w4 = ws[nt][g];
         const float y0 = ((float)acc[nt][mt][4 * g + 0] * am[mt]) * w4.x;
         const float y1 = ((float)acc[nt][mt][4 * g + 1] * am[mt]) * w4.y;
         const float y2 = ((float)acc[nt][mt][4 * g + 2] * am[mt]) * w4.z;
@@ -467,23 +460,24 @@ __global__ __launch_bounds__(kGThreads, 1) void w8a8_gemm_kernel(
   }
   // Each wave reads back only what it wrote itself: its LDS writes complete in order before
   // its reads (the compiler waits on lgkmcnt), so no barrier is needed here.
-  const int n_lane = n0 + wn * 128 + (lane & 15) * 8;
+  constexpr int kReads = kGWaveM / 4;
+  const int n_lane = n0 + wn * kGWaveN + (lane & 15) * 8;
   if constexpr (kQk) {
     // The wave's 128 channels are one head of the q|k|v thirds (N = 3 H 128, tiles 128-aligned);
     // each 16-lane row of a read-back is one token's finished bf16 head row -- the input of
     // qk_prep, rounded exactly as the unfused path stores it in Y.
-    const int head_g = (n0 + wn * 128) / flk::kQkHeadDim;
-    if (n0 + wn * 128 >= N) return;
+    const int head_g = (n0 + wn * kGWaveN) / flk::kQkHeadDim;
+    if (n0 + wn * kGWaveN >= N) return;
     const int sec = head_g / qe.heads, h = head_g - sec * qe.heads;
     const int l16 = lane & 15;
     float sc[8];
     if (sec < 2) flk::load_scale8<kScaleF32>(sec == 0 ? qe.q_scale : qe.k_scale, l16, sc);
     uint16_t* const out = qe.out[sec];
 #pragma unroll 4
-    for (int it = 0; it < 32; ++it) {
+    for (int it = 0; it < kReads; ++it) {
       const int ml = it * 4 + (lane >> 4);
       const uint4 v = *reinterpret_cast<const uint4*>(out_lds + ml * 256 + ((l16 ^ (ml & 15)) * 16));
-      const int m = m0 + wm * 128 + ml;
+      const int m = m0 + wm * kGWaveM + ml;
       if (m >= M) continue;   // uniform over the 16-lane row, so the DPP rows stay whole
       const int b = m / qe.length, t = m - b * qe.length;
       uint4 r = v;
@@ -501,10 +495,10 @@ __global__ __launch_bounds__(kGThreads, 1) void w8a8_gemm_kernel(
   }
   const bool wide = (y_stride & 7) == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0;   // 16-byte rows
 #pragma unroll 8
-  for (int it = 0; it < 32; ++it) {
+  for (int it = 0; it < kReads; ++it) {
     const int ml = it * 4 + (lane >> 4);
     const uint4 v = *reinterpret_cast<const uint4*>(out_lds + ml * 256 + (((lane & 15) ^ (ml & 15)) * 16));
-    const int m = m0 + wm * 128 + ml;
+    const int m = m0 + wm * kGWaveM + ml;
     if (m < M && n_lane < N) {
       uint16_t* dst = y + (int64_t)m * y_stride + n_lane;
       if (wide && n_lane + 8 <= N) {
