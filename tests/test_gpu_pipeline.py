@@ -112,3 +112,22 @@ def test_single_block_attention_section(device):
     print(describe("single block", st))
     assert st["max_abs"] <= MAX_ABS and st["mean_abs"] <= MEAN_ABS, st
     assert torch.equal(mlp.cpu(), lin1[..., 9216:])
+
+
+def test_path_2048_long_sequence_sampled(device):
+    """2048^2 Klein shape (512 text + 128x128 image tokens = 16896), full size on the GPU.
+    The oracle restates two heads for 512 query rows spread over the sequence (text and
+    image positions) against all 16896 keys -- attention rows are independent."""
+    w = workloads.WORKLOADS["klein_2048"]
+    qkv, qs, ks, ids, got = run_path(w, device)
+    assert np.isfinite(got).all()
+    heads_sel = [5, 17]
+    rows = np.unique(np.concatenate([np.arange(0, 512, 16), np.linspace(512, w.length - 1, 480).astype(int)]))
+    cols = [np.arange(s * w.num_heads * 128 + h * 128, s * w.num_heads * 128 + (h + 1) * 128)
+            for s in range(3) for h in heads_sel]
+    qkv_sel = to_np(qkv)[..., np.concatenate(cols)]
+    q, k, v = P.qk_prep_plain(qkv_sel, to_np(qs), to_np(ks), P.embed_nd(ids), len(heads_sel))
+    want = P.sdpa(q[:, :, rows], k, v)
+    st = abs_stats(got[:, heads_sel][:, :, rows], want)
+    print(describe("klein_2048 sampled", st))
+    assert st["max_abs"] <= MAX_ABS and st["mean_abs"] <= MEAN_ABS, st
