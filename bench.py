@@ -171,6 +171,11 @@ def w8a8_leg(args, timed, dev) -> dict:
 
     fused_ms = timed(fused, args.steps)
     unfused_ms = timed(unfused, args.steps)
+    # The block input's modulate (LayerNorm, scale, shift) fused into the quantisation.
+    g = torch.Generator().manual_seed(6)
+    shift = (0.3 * torch.randn(1, p.hidden, generator=g)).to(torch.bfloat16).to(dev)
+    scale = (0.1 * torch.randn(1, p.hidden, generator=g)).to(torch.bfloat16).to(dev)
+    mod_ms = timed(lambda i: w8a8.quantize_act_modulated(x3, shift, scale, qw.inv_smooth), args.steps)
     del x3
     return {"workload": f"{p.name}: X ({p.tokens}, {p.hidden}) bf16 with {p.outlier_fraction:.0%} outlier "
                         f"channels x{p.outlier_gain:g}, W ({p.hidden}, {p.out_features}) ~ N(0, 0.02)",
@@ -178,6 +183,7 @@ def w8a8_leg(args, timed, dev) -> dict:
                          "unit": "TOP/s", "frac": round(tops / INT8_DENSE_PEAK_TOPS, 4), "kernel": "w8a8_gemm_kernel",
                          "ops_per_launch": p.gemm_ops(), "avg_launch_us": round(gemm_ms * 1e3, 2)},
             "quantize_act_us": round(quant_ms * 1e3, 2),
+            "modulate_quantize_act_us": round(mod_ms * 1e3, 2),
             "gemm_then_qk_prep_us": round(unfused_ms * 1e3, 2),
             "fused_gemm_qk_prep_us": round(fused_ms * 1e3, 2),
             "dtype": "int8 operands, int32 accumulate, bf16 out"}

@@ -202,11 +202,29 @@ __global__ __launch_bounds__(256) void quantize_weight_kernel(const uint16_t* __
 
 // Activation (per forward): one wave per token row, the row held in registers
 // (kChunks x 8 elements per lane), absmax reduced across the wave.
-template <int kChunks>
+//
+// kModulate: the row is first the block input x and becomes the projection input
+//   X = bf16(bf16((bf16(1 + scale) * bf16(layer_norm(x)))) + shift)      (modules.py:38-40)
+// with layer_norm(x) = bf16((x - mean) * (1 / sqrt(var + 1e-6))) (nn.py:17-21), the mean and
+// the variance each summed in float64 and rounded to float32 once (bf16 inputs make the f64
+// sum of the row exact, so the mean does not depend on the summation order), every other
+// step one f32 operation.  scale / shift are the modulation rows of the token's batch entry;
+// X is optionally stored (bf16) for other consumers of the modulated input.
+__device__ __forceinline__ double wave_sum(double v) {
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d);
+  return v;
+}
+
+template <int kChunks, bool kModulate>
 __global__ __launch_bounds__(256) void quantize_act_kernel(const uint16_t* __restrict__ x, int64_t x_stride,
                                                            const float* __restrict__ inv_s, int M, int K,
                                                            int8_t* __restrict__ xq,
-                                                           float* __restrict__ a_scale) {
+                                                           float* __restrict__ a_scale,
+                                                           const uint16_t* __restrict__ shift,
+                                                           const uint16_t* __restrict__ scale,
+                                                           int64_t mod_stride, int tokens_per_batch,
+                                                           uint16_t* __restrict__ x_mod, int64_t x_mod_stride) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int row = blockIdx.x * 4 + wave;
   if (row >= M) return;
@@ -220,6 +238,53 @@ __global__ __launch_bounds__(256) void quantize_act_kernel(const uint16_t* __res
     if (idx < nch) v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src) + idx);
     raw[c] = uint4{v.x, v.y, v.z, v.w};
   }
+  float xr[kChunks][8];
+#pragma unroll
+  for (int c = 0; c < kChunks; ++c) unpack_bf16x8(raw[c], xr[c]);
+
+  if constexpr (kModulate) {
+    double sum = 0.0;
+#pragma unroll
+    for (int c = 0; c < kChunks; ++c)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) sum += (double)xr[c][i];   // padding lanes hold zeros
+    const float mean = (float)(wave_sum(sum) / (double)K);
+    double ssq = 0.0;
+#pragma unroll
+    for (int c = 0; c < kChunks; ++c) {
+      const bool valid = c * 64 + lane < nch;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        xr[c][i] = xr[c][i] - mean;
+        if (valid) ssq += (double)(xr[c][i] * xr[c][i]);
+      }
+    }
+    const float var = (float)(wave_sum(ssq) / (double)K);
+    const float inv = 1.0f / sqrtf(var + 1e-6f);
+    const int b = row / tokens_per_batch;
+    const uint16_t* sh = shift + (int64_t)b * mod_stride;
+    const uint16_t* sc = scale + (int64_t)b * mod_stride;
+    uint16_t* xm = x_mod ? x_mod + (int64_t)row * x_mod_stride : nullptr;
+#pragma unroll
+    for (int c = 0; c < kChunks; ++c) {
+      const int idx = c * 64 + lane;
+      if (idx >= nch) continue;
+      float sf[8], tf[8];
+      unpack_bf16x8(*reinterpret_cast<const uint4*>(sh + idx * 8), sf);
+      unpack_bf16x8(*reinterpret_cast<const uint4*>(sc + idx * 8), tf);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float base = flk::round_bf16(xr[c][i] * inv);
+        const float one_plus = flk::round_bf16(1.0f + tf[i]);
+        xr[c][i] = flk::round_bf16(flk::round_bf16(one_plus * base) + sf[i]);
+      }
+      if (xm)
+        *reinterpret_cast<uint4*>(xm + idx * 8) =
+            uint4{flk::pack_bf16x2(xr[c][0], xr[c][1]), flk::pack_bf16x2(xr[c][2], xr[c][3]),
+                  flk::pack_bf16x2(xr[c][4], xr[c][5]), flk::pack_bf16x2(xr[c][6], xr[c][7])};
+    }
+  }
+
   float xh[kChunks][8];
   float amax = 0.0f;
 #pragma unroll
@@ -227,12 +292,10 @@ __global__ __launch_bounds__(256) void quantize_act_kernel(const uint16_t* __res
     const int idx = c * 64 + lane;
     const f32x4 s0 = idx < nch ? reinterpret_cast<const f32x4*>(inv_s)[2 * idx] : f32x4{0, 0, 0, 0};
     const f32x4 s1 = idx < nch ? reinterpret_cast<const f32x4*>(inv_s)[2 * idx + 1] : f32x4{0, 0, 0, 0};
-    float f[8];
-    unpack_bf16x8(raw[c], f);
     const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      xh[c][i] = f[i] * sv[i];
+      xh[c][i] = xr[c][i] * sv[i];
       amax = fmaxf(amax, fabsf(xh[c][i]));
     }
   }
@@ -568,6 +631,27 @@ extern "C" int flk_quantize_weight(const void* w, int64_t w_row_stride, const fl
   return flk_launch_status();
 }
 
+namespace {
+
+template <bool kModulate>
+void launch_quantize_act(int chunks, dim3 grid, hipStream_t st, const uint16_t* xs, int64_t xstride,
+                         const float* inv_s, int m, int k, int8_t* xq, float* a_scale, const uint16_t* shift,
+                         const uint16_t* scale, int64_t mod_stride, int tokens, uint16_t* x_mod, int64_t xm_stride) {
+  const dim3 block(256);
+#define FLK_QA(C) hipLaunchKernelGGL((quantize_act_kernel<C, kModulate>), grid, block, 0, st, xs, xstride, inv_s, m, k, \
+                                     xq, a_scale, shift, scale, mod_stride, tokens, x_mod, xm_stride)
+  if (chunks <= 1) FLK_QA(1);
+  else if (chunks <= 2) FLK_QA(2);
+  else if (chunks <= 4) FLK_QA(4);
+  else if (chunks <= 6) FLK_QA(6);
+  else if (chunks <= 8) FLK_QA(8);
+  else if (chunks <= 12) FLK_QA(12);
+  else FLK_QA(16);
+#undef FLK_QA
+}
+
+}  // namespace
+
 extern "C" int flk_quantize_act(const void* x, int64_t x_row_stride, const float* inv_s, int m, int k,
                                 int8_t* xq, float* a_scale, void* stream) {
   if (m < 0 || k < 0 || x_row_stride < k) return FLK_E_INVALID;
@@ -577,17 +661,31 @@ extern "C" int flk_quantize_act(const void* x, int64_t x_row_stride, const float
   if (x_row_stride % 8 || !flk_host_aligned(x, 16) || !flk_host_aligned(inv_s, 16) || !flk_host_aligned(xq, 8) ||
       !flk_host_aligned(a_scale, 4))
     return FLK_E_ALIGN;
-  const int chunks = (k / 8 + 63) / 64;
-  const dim3 grid((unsigned)((m + 3) / 4)), block(256);
-  const hipStream_t st = as_stream(stream);
-  const uint16_t* xs = static_cast<const uint16_t*>(x);
-  if (chunks <= 1)       hipLaunchKernelGGL(quantize_act_kernel<1>, grid, block, 0, st, xs, x_row_stride, inv_s, m, k, xq, a_scale);
-  else if (chunks <= 2)  hipLaunchKernelGGL(quantize_act_kernel<2>, grid, block, 0, st, xs, x_row_stride, inv_s, m, k, xq, a_scale);
-  else if (chunks <= 4)  hipLaunchKernelGGL(quantize_act_kernel<4>, grid, block, 0, st, xs, x_row_stride, inv_s, m, k, xq, a_scale);
-  else if (chunks <= 6)  hipLaunchKernelGGL(quantize_act_kernel<6>, grid, block, 0, st, xs, x_row_stride, inv_s, m, k, xq, a_scale);
-  else if (chunks <= 8)  hipLaunchKernelGGL(quantize_act_kernel<8>, grid, block, 0, st, xs, x_row_stride, inv_s, m, k, xq, a_scale);
-  else if (chunks <= 12) hipLaunchKernelGGL(quantize_act_kernel<12>, grid, block, 0, st, xs, x_row_stride, inv_s, m, k, xq, a_scale);
-  else                   hipLaunchKernelGGL(quantize_act_kernel<16>, grid, block, 0, st, xs, x_row_stride, inv_s, m, k, xq, a_scale);
+  launch_quantize_act<false>((k / 8 + 63) / 64, dim3((unsigned)((m + 3) / 4)), as_stream(stream),
+                             static_cast<const uint16_t*>(x), x_row_stride, inv_s, m, k, xq, a_scale, nullptr,
+                             nullptr, 0, 1, nullptr, 0);
+  return flk_launch_status();
+}
+
+extern "C" int flk_quantize_act_modulated(const void* x, int64_t x_row_stride, const void* shift,
+                                          const void* scale, int64_t mod_batch_stride, int tokens_per_batch,
+                                          const float* inv_s, int m, int k, int8_t* xq, float* a_scale,
+                                          void* x_mod, int64_t x_mod_row_stride, void* stream) {
+  if (m < 0 || k < 0 || x_row_stride < k || tokens_per_batch <= 0 || mod_batch_stride < 0 ||
+      (x_mod && x_mod_row_stride < k))
+    return FLK_E_INVALID;
+  if (m == 0 || k == 0) return FLK_OK;
+  if (!x || !shift || !scale || !inv_s || !xq || !a_scale) return FLK_E_INVALID;
+  if ((m - 1) / tokens_per_batch > 0 && mod_batch_stride < k) return FLK_E_INVALID;
+  if (k % 8 || k > 8192) return FLK_E_UNSUPPORTED;
+  if (x_row_stride % 8 || mod_batch_stride % 8 || !flk_host_aligned(x, 16) || !flk_host_aligned(shift, 16) ||
+      !flk_host_aligned(scale, 16) || !flk_host_aligned(inv_s, 16) || !flk_host_aligned(xq, 8) ||
+      !flk_host_aligned(a_scale, 4) || (x_mod && (!flk_host_aligned(x_mod, 16) || x_mod_row_stride % 8)))
+    return FLK_E_ALIGN;
+  launch_quantize_act<true>((k / 8 + 63) / 64, dim3((unsigned)((m + 3) / 4)), as_stream(stream),
+                            static_cast<const uint16_t*>(x), x_row_stride, inv_s, m, k, xq, a_scale,
+                            static_cast<const uint16_t*>(shift), static_cast<const uint16_t*>(scale), mod_batch_stride,
+                            tokens_per_batch, static_cast<uint16_t*>(x_mod), x_mod_row_stride);
   return flk_launch_status();
 }
 

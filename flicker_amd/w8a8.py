@@ -133,6 +133,42 @@ def quantize_act(x: torch.Tensor, inv_smooth: torch.Tensor) -> tuple[torch.Tenso
     return xq, a_scale
 
 
+def quantize_act_modulated(x: torch.Tensor, shift: torch.Tensor, scale: torch.Tensor, inv_smooth: torch.Tensor,
+                           *, x_mod: torch.Tensor | bool | None = None):
+    """int8 activation of the modulated block input in one pass: X = modulate(x, shift, scale)
+    (modules.py:38-40: (1 + scale) * layer_norm(x) + shift, bf16) then quantize_act(X).
+
+    x (B, L, K) bf16 block input; shift, scale (B, K) bf16 modulation rows (the reference's
+    (B, 1, K) ``ModTriple`` entries).  Returns (xq (B*L, K) int8, a_scale (B*L,) f32), plus X
+    (B, L, K) bf16 when ``x_mod`` is True or a tensor to write it into."""
+    if x.dim() != 3:
+        raise ValueError(f"x must be (B, L, K), got {tuple(x.shape)}")
+    batch, length, k = x.shape
+    shift = shift.reshape(batch, k) if shift.dim() == 3 else shift
+    scale = scale.reshape(batch, k) if scale.dim() == 3 else scale
+    for name, t in (("shift", shift), ("scale", scale)):
+        _on_gpu(name, t)
+        if t.dtype != torch.bfloat16 or t.shape != (batch, k):
+            raise ValueError(f"{name} must be bfloat16 ({batch}, {k}) (or ({batch}, 1, {k}))")
+    shift, scale = shift.contiguous(), scale.contiguous()
+    xr = _rows("x", x)
+    inv = _f32("inv_smooth", inv_smooth, k, x.device)
+    m = batch * length
+    xq = torch.empty((m, k), dtype=torch.int8, device=x.device)
+    a_scale = torch.empty(m, dtype=torch.float32, device=x.device)
+    out = None
+    if x_mod is True:
+        out = torch.empty((batch, length, k), dtype=torch.bfloat16, device=x.device)
+    elif isinstance(x_mod, torch.Tensor):
+        out = x_mod
+        if out.shape != (batch, length, k) or out.dtype != torch.bfloat16 or not out.is_contiguous():
+            raise ValueError(f"x_mod must be a contiguous bfloat16 ({batch}, {length}, {k}) tensor")
+    _lib.check(_lib.lib().flk_quantize_act_modulated(
+        xr.data_ptr(), xr.stride(0), shift.data_ptr(), scale.data_ptr(), shift.stride(0), length, inv.data_ptr(),
+        m, k, xq.data_ptr(), a_scale.data_ptr(), _lib.ptr(out), k, _lib.stream_of(x)), "flk_quantize_act_modulated")
+    return (xq, a_scale) if out is None else (xq, a_scale, out)
+
+
 def gemm(xq: torch.Tensor, a_scale: torch.Tensor, wq_t: torch.Tensor, w_scale: torch.Tensor, *,
          out: torch.Tensor | None = None, acc: torch.Tensor | None = None) -> torch.Tensor:
     """Y (M, N) bf16 = bf16((f32(xq . wq_t^T) * a_scale) * w_scale).  ``out`` may be a row-strided
@@ -169,12 +205,17 @@ def linear(x: torch.Tensor, qw: QuantizedLinear, *, out: torch.Tensor | None = N
 
 
 def qk_prep(x: torch.Tensor, qw: QuantizedLinear, q_scale: torch.Tensor, k_scale: torch.Tensor, freqs,
-            num_heads: int, *, out=None, out_offset: int = 0):
+            num_heads: int, *, out=None, out_offset: int = 0, modulation=None):
     """``kernels.qk_prep(linear(x, qw), q_scale, k_scale, freqs, num_heads)`` in two launches
     instead of three: the activation quantisation, then one int8 GEMM whose epilogue applies
     QK-RMSNorm + RoPE (+ q_gain) to each finished head row and writes head-major q, k, v
     (kernels.py:57-91 after nn.py:13-14); the projected activation never reaches memory.
-    Bit-identical to the unfused pair.  x (B, L, K) bf16 -> q, k, v (B, H, L, 128) bf16."""
+    Bit-identical to the unfused pair.  x (B, L, K) bf16 -> q, k, v (B, H, L, 128) bf16.
+
+    With ``modulation=(shift, scale)`` x is the raw block input and the projection input is
+    modulate(x, shift, scale) (modules.py:38-40), computed inside the activation quantisation:
+    the whole ``qkv_prep(linear(modulate(x, mod1), w), ...)`` of a block (modules.py:128-133,
+    186-190) is then two launches."""
     from .kernels import HEAD_DIM, Freqs
 
     if x.dim() != 3:
@@ -193,7 +234,10 @@ def qk_prep(x: torch.Tensor, qw: QuantizedLinear, q_scale: torch.Tensor, k_scale
             or q_scale.numel() != HEAD_DIM or k_scale.numel() != HEAD_DIM:
         raise ValueError(f"q_scale / k_scale must be {HEAD_DIM} bfloat16 or float32 values of one dtype")
     q_scale, k_scale = q_scale.reshape(-1).contiguous(), k_scale.reshape(-1).contiguous()
-    xq, a_scale = quantize_act(x, qw.inv_smooth)
+    if modulation is None:
+        xq, a_scale = quantize_act(x, qw.inv_smooth)
+    else:
+        xq, a_scale = quantize_act_modulated(x, modulation[0], modulation[1], qw.inv_smooth)
     if out is None:
         if out_offset:
             raise ValueError("out_offset needs out=(q, k, v)")

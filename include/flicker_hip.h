@@ -136,6 +136,19 @@ int flk_quantize_weight(const void* w, int64_t w_row_stride, const float* s, int
 int flk_quantize_act(const void* x, int64_t x_row_stride, const float* inv_s, int m, int k,
                      int8_t* xq, float* a_scale, void* stream);
 
+/* flk_quantize_act of the modulated block input: X = modulate(x) (src/flicker/modules.py:38-40,
+ * norm=True: (1 + scale) * layer_norm(x) + shift, each bf16 operation rounded; layer_norm per
+ * src/flicker/nn.py:17-21 with its mean and variance summed in float64 and rounded to float32
+ * once) is computed from the raw x and quantised in the same pass.  Replaces the reference's
+ * modulate(...) feeding linear(., qkv.weight) (modules.py:128,132,186).
+ *   x (m, k) bf16 (row stride in elements); token row r belongs to batch entry
+ *   r / tokens_per_batch, whose modulation rows are shift / scale + entry * mod_batch_stride
+ *   (k bf16 values each).  x_mod (optional, NULL to skip) receives X as bf16 (m, k).
+ * k % 8 == 0, k <= 8192; strides multiples of 8; shift, scale, x_mod 16-byte aligned. */
+int flk_quantize_act_modulated(const void* x, int64_t x_row_stride, const void* shift, const void* scale,
+                               int64_t mod_batch_stride, int tokens_per_batch, const float* inv_s, int m, int k,
+                               int8_t* xq, float* a_scale, void* x_mod, int64_t x_mod_row_stride, void* stream);
+
 /* y (m, n) bf16 = rescaled int8 product of xq (m, k) and wq_t (n, k); when acc_or_null is
  * given, the exact int32 products are also written there as (m, n).  k % 128 == 0,
  * n % 4 == 0, y 8-byte aligned with y_row_stride % 4 == 0. */

@@ -101,3 +101,29 @@ def w8a8_linear(x, inv_s, wq, w_scale):
     xq, a_scale = quantize_act(x, inv_s)
     acc = int_gemm(xq, wq)
     return rescale(acc, a_scale, w_scale), acc, xq, a_scale
+
+
+# --------------------------------------------------------- block input: LayerNorm + modulate
+def layer_norm(x, eps: float = 1e-6) -> np.ndarray:
+    """nn.py:17-21 -- bf16((x - mean) * rsqrt(var + eps)) over the last axis, with the mean and
+    the variance each accumulated in f64 and rounded to f32 once (the order-free ideal of
+    XLA's f32 reductions); x - mean, its square and the product are single f32 operations and
+    rsqrt is 1/sqrt in f32, as for rms_norm (path.py)."""
+    xf = np.asarray(x, dtype=F32)
+    mean = np.mean(xf.astype(np.float64), axis=-1, keepdims=True).astype(F32)
+    d = (xf - mean).astype(F32)
+    sq = (d * d).astype(F32)
+    var = np.mean(sq.astype(np.float64), axis=-1, keepdims=True).astype(F32)
+    inv = F32(1.0) / np.sqrt(var + F32(eps), dtype=F32)
+    return bf16_round((d * inv).astype(F32))
+
+
+def modulate(x, shift, scale) -> np.ndarray:
+    """modules.py:38-40 with norm=True -- (1 + scale) * layer_norm(x) + shift in bf16: each
+    of the three bf16 operations rounds its f32 result to bf16.  x (B, L, K); shift, scale
+    (B, K) (the reference's (B, 1, K) modulation rows)."""
+    base = layer_norm(x)
+    shift = np.asarray(shift, dtype=F32)[:, None, :]
+    scale = np.asarray(scale, dtype=F32)[:, None, :]
+    one_plus = bf16_round((F32(1.0) + scale).astype(F32))
+    return bf16_round((bf16_round((one_plus * base).astype(F32)) + shift).astype(F32))

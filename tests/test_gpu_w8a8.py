@@ -252,6 +252,44 @@ def test_fused_projection_writes_at_sequence_offset(device):
         assert bool((a[:, :, :20] == 3.0).all()) and bool((a[:, :, 84:] == 3.0).all())
 
 
+@pytest.mark.parametrize("batch,length,k", [(2, 300, 3072), (1, 5, 200), (3, 17, 512)])
+def test_modulated_activation_bit_exact(device, batch, length, k):
+    """flk_quantize_act_modulated: X = modulate(x) (modules.py:38-40) equals the oracle bit for
+    bit (f64 row statistics make the mean order-free), and its int8 quantisation equals both
+    the oracle's and the unfused quantize_act of that X."""
+    g = torch.Generator().manual_seed(k + length)
+    x = 2.0 * torch.randn(batch, length, k, generator=g) + 0.3
+    x[..., 7] *= 15.0                                                 # an outlier channel
+    shift = 0.5 * torch.randn(batch, k, generator=g)
+    scale = 0.2 * torch.randn(batch, k, generator=g)
+    x, shift, scale = (t.to(torch.bfloat16) for t in (x, shift, scale))
+    inv_s = (0.5 + torch.rand(k, generator=g)).to(device)
+    xq, a_scale, x_mod = w8a8.quantize_act_modulated(x.to(device), shift.to(device), scale.to(device), inv_s,
+                                                     x_mod=True)
+    want_mod = Q.modulate(host_f32(x), host_f32(shift), host_f32(scale))
+    assert_bits_equal(x_mod, want_mod, "modulated X")
+    want_q, want_a = Q.quantize_act(want_mod.reshape(-1, k), host(inv_s))
+    np.testing.assert_array_equal(host(xq), want_q)
+    np.testing.assert_array_equal(host(a_scale), want_a)
+    xq2, a2 = w8a8.quantize_act(x_mod, inv_s)
+    assert torch.equal(xq2, xq) and torch.equal(a2, a_scale)
+
+
+def test_modulated_projection_qk_prep(device):
+    """The whole qkv_prep(linear(modulate(x, mod1), w), ...) of a block in two launches equals
+    the step-by-step path (modulated X, then the fused projection + qk_prep)."""
+    x, qw, qs, ks, freqs, kernels = _fused_case(device, 1, 300, 3, 256, torch.bfloat16, 0.3, seed=21)
+    g = torch.Generator().manual_seed(22)
+    shift = (0.3 * torch.randn(1, 256, generator=g)).to(torch.bfloat16).to(device)
+    scale = (0.1 * torch.randn(1, 256, generator=g)).to(torch.bfloat16).to(device)
+    got = w8a8.qk_prep(x, qw, qs, ks, freqs, 3, modulation=(shift, scale))
+    _, _, x_mod = w8a8.quantize_act_modulated(x, shift, scale, qw.inv_smooth, x_mod=True)
+    want = w8a8.qk_prep(x_mod, qw, qs, ks, freqs, 3)
+    torch.cuda.synchronize()
+    for a, b in zip(got, want):
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
 def test_errors(device):
     x = torch.zeros((4, 100), dtype=torch.bfloat16, device=device)
     with pytest.raises(Exception, match="status -3"):        # k % 8

@@ -306,3 +306,42 @@ def test_w8a8_error_is_small_against_bf16_linear():
     ref = x.astype(np.float64) @ w.astype(np.float64)
     rel = np.linalg.norm(y - ref) / np.linalg.norm(ref)
     assert rel < 0.03, rel
+
+
+def _layer_norm_loop(row):
+    """Element loop in exact rationals where possible: f64 mean/variance of the f32 values,
+    each rounded to f32, then per element f32 subtract, square, product and bf16 rounding."""
+    vals = [float(np.float32(v)) for v in row]
+    mean = np.float32(sum(vals) / len(vals))
+    d = [np.float32(np.float32(v) - mean) for v in vals]
+    var = np.float32(sum(float(np.float32(e * e)) for e in d) / len(d))
+    inv = np.float32(1.0) / np.float32(math.sqrt(np.float32(var + np.float32(1e-6))))
+    return np.array([bf16_round(np.float32(e * inv)) for e in d], dtype=np.float32)
+
+
+def test_layer_norm_bruteforce_and_invariants():
+    rng = np.random.default_rng(11)
+    x = bf16_round((3.0 * rng.standard_normal((4, 2, 96)) + 0.7).astype(np.float32))
+    got = Q.layer_norm(x)
+    for idx in np.ndindex(x.shape[:-1]):
+        np.testing.assert_array_equal(got[idx], _layer_norm_loop(x[idx]))
+    # unit statistics before rounding, a constant row normalises to zero
+    assert np.abs(got.mean(-1)).max() < 0.02 and np.abs(got.var(-1) - 1).max() < 0.02
+    np.testing.assert_array_equal(Q.layer_norm(np.full((1, 1, 64), 2.5, np.float32)), 0.0)
+
+
+def test_modulate_known_answers():
+    rng = np.random.default_rng(12)
+    x = bf16_round(rng.standard_normal((2, 5, 64)).astype(np.float32))
+    zero = np.zeros((2, 64), np.float32)
+    np.testing.assert_array_equal(Q.modulate(x, zero, zero), Q.layer_norm(x))            # identity modulation
+    shift = bf16_round(rng.standard_normal((2, 64)).astype(np.float32))
+    np.testing.assert_array_equal(Q.modulate(x, shift, np.full((2, 64), -1.0, np.float32)),
+                                  np.broadcast_to(shift[:, None, :], x.shape))            # scale -1 keeps the shift
+    scale = bf16_round(0.1 * rng.standard_normal((2, 64)).astype(np.float32))
+    got = Q.modulate(x, shift, scale)
+    base = Q.layer_norm(x)
+    for b, t, j in np.ndindex(x.shape):      # per-element loop of the three bf16 roundings
+        one = bf16_round(np.float32(1.0) + np.float32(scale[b, j]))
+        want = bf16_round(np.float32(bf16_round(np.float32(one * base[b, t, j])) + np.float32(shift[b, j])))
+        assert got[b, t, j] == want
