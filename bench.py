@@ -215,6 +215,7 @@ def main() -> int:
     ids = workloads.make_ids(w)
     qs, ks = qs_cpu.to(dev), ks_cpu.to(dev)
     freqs = rope.rope_lanes(ids, workloads.q_gain(w), device=dev)
+    positions = rope.position_ids(ids, workloads.q_gain(w), device=dev)
 
     act_bytes = qkv_cpu.numel() * 2
     set_bytes = 2 * act_bytes + act_bytes // 3
@@ -235,6 +236,10 @@ def main() -> int:
     def run_qk(i):
         qkv, out, _ = sets[i % n_sets]
         kernels.qk_prep(qkv, qs, ks, freqs, w.num_heads, out=out)
+
+    def run_qk_ids(i):   # the same qk_prep with its RoPE lanes computed from the ids in-kernel
+        qkv, out, _ = sets[i % n_sets]
+        kernels.qk_prep(qkv, qs, ks, positions, w.num_heads, out=out)
 
     def run_attend(i):
         _, out, o = sets[i % n_sets]
@@ -267,6 +272,7 @@ def main() -> int:
     qk_ms = timed(run_qk, args.steps) if args.only == "step" else step_ms
     at_ms = timed(run_attend, args.steps) if args.only == "step" else step_ms
     qk_gbs = w.qk_prep_bytes() / (qk_ms * 1e-3) / 1e9
+    qk_ids_ms = timed(run_qk_ids, args.steps) if args.only == "step" else None
     at_tflops = w.attend_flops() / (at_ms * 1e-3) / 1e12
 
     traffic = {}
@@ -303,6 +309,11 @@ def main() -> int:
                                  "traffic_source": source, "kernel": "qk_prep_kernel",
                                  "bytes_per_launch": w.qk_prep_bytes(), "avg_launch_us": round(qk_ms * 1e3, 2)}},
     }
+    if qk_ids_ms is not None:
+        ids_gbs = w.qk_prep_bytes(tables=False) / (qk_ids_ms * 1e-3) / 1e9
+        result["qk_prep"]["position_ids"] = {
+            "avg_launch_us": round(qk_ids_ms * 1e3, 2), "bytes_per_launch": w.qk_prep_bytes(tables=False),
+            "achieved": round(ids_gbs, 1), "unit": "GB/s", "frac": round(ids_gbs / HBM_PEAK_GBS, 4)}
     if not args.no_w8a8 and args.only == "step":
         result["w8a8"] = w8a8_leg(args, timed, dev)
     if not args.no_cpu_baseline and args.only == "step":

@@ -19,9 +19,15 @@
 // read once) before any math, and keeps the token's cos/sin lanes in registers across
 // those heads.
 //
+// The RoPE lanes come from one of two sources: the (L, 128) f32 cos / sin tables
+// (kernels.py:28-31), or -- flk_qk_prep_ids -- the token's position ids, from which each
+// lane computes the cos / sin of its 4 pairs (rope.py:9-21) while its loads are in flight,
+// with the same arithmetic as the table kernels (rope_math.h), so both give identical bits.
+//
 // The kernel is HBM-bound: per (b, t, h) it moves 3*256 bytes in and 3*256 out.
 
 #include "qk_math.h"
+#include "rope_math.h"
 
 namespace {
 
@@ -41,6 +47,21 @@ constexpr int kTokensPerBlock = kThreads / kLanesPerRow;
 #ifndef FLK_QK_HPG
 #define FLK_QK_HPG 0
 #endif
+#ifndef FLK_QK_IDS_HPG
+#define FLK_QK_IDS_HPG 0
+#endif
+
+// Where the RoPE lanes of token t come from: tables (cos / sin rows of table_stride floats)
+// or position ids (rows of ids_stride floats, one per axis of ax).
+struct RopeSource {
+  const float* cos;
+  const float* sin;
+  int64_t table_stride;
+  const float* ids;
+  int64_t ids_stride;
+  flk::Axes ax;
+  float theta;
+};
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
@@ -61,10 +82,9 @@ __device__ __forceinline__ void store16(uint16_t* p, uint4 v) {
   }
 }
 
-template <bool kScaleF32, bool kGain, int kHeads>
+template <bool kScaleF32, bool kGain, int kHeads, bool kIds>
 __global__ __launch_bounds__(kThreads) void qk_prep_kernel(
-    const uint16_t* __restrict__ qkv, int64_t batch_stride, int64_t row_stride,
-    const float* __restrict__ cos_t, const float* __restrict__ sin_t, int64_t table_stride,
+    const uint16_t* __restrict__ qkv, int64_t batch_stride, int64_t row_stride, RopeSource rope,
     const void* __restrict__ q_scale, const void* __restrict__ k_scale, float q_gain,
     int length, int num_heads, uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_out,
     uint16_t* __restrict__ v_out, int64_t out_length, int64_t out_offset) {
@@ -83,8 +103,25 @@ __global__ __launch_bounds__(kThreads) void qk_prep_kernel(
     rv[i] = load16(row + (int64_t)(2 * num_heads + h0 + i) * kHeadDim);
   }
   float c[8], s[8], qs[8], ks[8];
-  flk::load_table8(cos_t + (int64_t)t * table_stride, lane, c);
-  flk::load_table8(sin_t + (int64_t)t * table_stride, lane, s);
+  if constexpr (kIds) {
+    // lane l holds lane-table columns 8l .. 8l+7 = pairs 4l .. 4l+3:
+    // cos column 2p, 2p+1 = cos(angle_p); sin columns = -sin(angle_p), +sin(angle_p)
+    const float* pos = rope.ids + (int64_t)t * rope.ids_stride;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      int axis;
+      const float omega = flk::pair_omega(lane * 4 + j, rope.ax, rope.theta, axis);
+      float cj, sj;
+      flk::pair_cos_sin(pos[axis], omega, cj, sj);
+      c[2 * j] = cj;
+      c[2 * j + 1] = cj;
+      s[2 * j] = -sj;
+      s[2 * j + 1] = sj;
+    }
+  } else {
+    flk::load_table8(rope.cos + (int64_t)t * rope.table_stride, lane, c);
+    flk::load_table8(rope.sin + (int64_t)t * rope.table_stride, lane, s);
+  }
   flk::load_scale8<kScaleF32>(q_scale, lane, qs);
   flk::load_scale8<kScaleF32>(k_scale, lane, ks);
 
@@ -98,15 +135,24 @@ __global__ __launch_bounds__(kThreads) void qk_prep_kernel(
   }
 }
 
-template <bool kScaleF32, bool kGain>
-int launch(int heads_per_group, dim3 grid, hipStream_t stream, const uint16_t* qkv,
-           int64_t bs, int64_t rs, const float* cos_t, const float* sin_t, int64_t ts,
-           const void* qsc, const void* ksc, float gain, int length, int num_heads,
-           uint16_t* q, uint16_t* k, uint16_t* v, int64_t out_len, int64_t out_off) {
-#define FLK_QK_LAUNCH(NH)                                                                    \
-  hipLaunchKernelGGL((qk_prep_kernel<kScaleF32, kGain, NH>), grid, dim3(kThreads), 0, stream, \
-                     qkv, bs, rs, cos_t, sin_t, ts, qsc, ksc, gain, length, num_heads, q, k, v, \
-                     out_len, out_off)
+struct Launch {
+  const uint16_t* qkv;
+  int64_t batch_stride, row_stride;
+  RopeSource rope;
+  const void* q_scale;
+  const void* k_scale;
+  float q_gain;
+  int length, num_heads;
+  uint16_t *q, *k, *v;
+  int64_t out_length, out_offset;
+};
+
+template <bool kScaleF32, bool kGain, bool kIds>
+void launch(int heads_per_group, dim3 grid, hipStream_t stream, const Launch& a) {
+#define FLK_QK_LAUNCH(NH)                                                                       \
+  hipLaunchKernelGGL((qk_prep_kernel<kScaleF32, kGain, NH, kIds>), grid, dim3(kThreads), 0,     \
+                     stream, a.qkv, a.batch_stride, a.row_stride, a.rope, a.q_scale, a.k_scale, \
+                     a.q_gain, a.length, a.num_heads, a.q, a.k, a.v, a.out_length, a.out_offset)
   switch (heads_per_group) {
     case 6: FLK_QK_LAUNCH(6); break;
     case 4: FLK_QK_LAUNCH(4); break;
@@ -115,7 +161,55 @@ int launch(int heads_per_group, dim3 grid, hipStream_t stream, const uint16_t* q
     default: FLK_QK_LAUNCH(1); break;
   }
 #undef FLK_QK_LAUNCH
+}
+
+// Checks shared by both entry points: FLK_OK = launch, kEmpty = nothing to do (an empty
+// batch or sequence is accepted before any pointer or stride check), else an error status.
+constexpr int kEmpty = 1;
+
+int check_common(const void* qkv, int64_t qkv_batch_stride, int64_t qkv_row_stride,
+                 const void* q_scale, const void* k_scale, int batch, int length, int num_heads,
+                 int head_dim, const void* q_out, const void* k_out, const void* v_out,
+                 int64_t out_length, int64_t out_offset) {
+  if (head_dim != kHeadDim) return FLK_E_UNSUPPORTED;
+  if (batch < 0 || length < 0 || num_heads <= 0 || out_offset < 0 ||
+      out_offset + length > out_length)
+    return FLK_E_INVALID;
+  if (batch == 0 || length == 0) return kEmpty;
+  if (qkv_row_stride < 3LL * num_heads * head_dim ||
+      (batch > 1 && qkv_batch_stride < (int64_t)(length - 1) * qkv_row_stride + 3LL * num_heads * head_dim))
+    return FLK_E_INVALID;
+  if (!qkv || !q_scale || !k_scale || !q_out || !k_out || !v_out) return FLK_E_INVALID;
+  if (qkv_row_stride % 8 || qkv_batch_stride % 8 || !flk_host_aligned(qkv, 16) ||
+      !flk_host_aligned(q_scale, 16) || !flk_host_aligned(k_scale, 16) ||
+      !flk_host_aligned(q_out, 16) || !flk_host_aligned(k_out, 16) || !flk_host_aligned(v_out, 16))
+    return FLK_E_ALIGN;
+  return FLK_OK;
+}
+
+template <bool kIds>
+int dispatch(int hpg, int batch, int scale_is_f32, hipStream_t stream, const Launch& a) {
+  const dim3 grid((a.length + kTokensPerBlock - 1) / kTokensPerBlock, a.num_heads / hpg, batch);
+  const bool gain = a.q_gain != 1.0f;
+  if (scale_is_f32) {
+    if (gain) launch<true, true, kIds>(hpg, grid, stream, a);
+    else launch<true, false, kIds>(hpg, grid, stream, a);
+  } else {
+    if (gain) launch<false, true, kIds>(hpg, grid, stream, a);
+    else launch<false, false, kIds>(hpg, grid, stream, a);
+  }
   return flk_launch_status();
+}
+
+// Heads per 16-lane group.  With tables, two measured best at the Klein shapes (6 loads in
+// flight per lane and 2x more blocks than four heads per group).  With ids, each group
+// computes 4 powf + 4 cos/sin pairs per token, so four heads (measured at 1024^2: 36.3 us
+// against 39.7 us for two, 36.9 us for six) share that work across 12 rows.
+int heads_per_group(int num_heads, bool ids, int forced) {
+  int hpg = (num_heads % 2 == 0) ? 2 : (num_heads % 3 == 0) ? 3 : 1;
+  if (ids && num_heads % 4 == 0) hpg = 4;
+  if (forced > 0 && num_heads % forced == 0) hpg = forced;
+  return hpg;
 }
 
 }  // namespace
@@ -126,45 +220,64 @@ extern "C" int flk_qk_prep(const void* qkv, int64_t qkv_batch_stride, int64_t qk
                            float q_gain, int batch, int length, int num_heads, int head_dim,
                            void* q_out, void* k_out, void* v_out, int64_t out_length,
                            int64_t out_offset, void* stream) {
-  if (head_dim != kHeadDim) return FLK_E_UNSUPPORTED;
-  if (batch < 0 || length < 0 || num_heads <= 0 || out_offset < 0 ||
-      out_offset + length > out_length)
-    return FLK_E_INVALID;
-  if (batch == 0 || length == 0) return FLK_OK;
-  if (qkv_row_stride < 3LL * num_heads * head_dim || table_row_stride < head_dim ||
-      (batch > 1 && qkv_batch_stride < (int64_t)(length - 1) * qkv_row_stride + 3LL * num_heads * head_dim))
-    return FLK_E_INVALID;
-  if (!qkv || !cos || !sin || !q_scale || !k_scale || !q_out || !k_out || !v_out)
-    return FLK_E_INVALID;
-  if (qkv_row_stride % 8 || qkv_batch_stride % 8 || table_row_stride % 4 ||
-      !flk_host_aligned(qkv, 16) || !flk_host_aligned(cos, 16) || !flk_host_aligned(sin, 16) ||
-      !flk_host_aligned(q_scale, 16) || !flk_host_aligned(k_scale, 16) ||
-      !flk_host_aligned(q_out, 16) || !flk_host_aligned(k_out, 16) || !flk_host_aligned(v_out, 16))
+  const int st = check_common(qkv, qkv_batch_stride, qkv_row_stride, q_scale, k_scale, batch,
+                              length, num_heads, head_dim, q_out, k_out, v_out, out_length, out_offset);
+  if (st != FLK_OK) return st == kEmpty ? FLK_OK : st;
+  if (table_row_stride < head_dim || !cos || !sin) return FLK_E_INVALID;
+  if (table_row_stride % 4 || !flk_host_aligned(cos, 16) || !flk_host_aligned(sin, 16))
     return FLK_E_ALIGN;
+  Launch a{};
+  a.qkv = static_cast<const uint16_t*>(qkv);
+  a.batch_stride = qkv_batch_stride;
+  a.row_stride = qkv_row_stride;
+  a.rope.cos = cos;
+  a.rope.sin = sin;
+  a.rope.table_stride = table_row_stride;
+  a.q_scale = q_scale;
+  a.k_scale = k_scale;
+  a.q_gain = q_gain;
+  a.length = length;
+  a.num_heads = num_heads;
+  a.q = static_cast<uint16_t*>(q_out);
+  a.k = static_cast<uint16_t*>(k_out);
+  a.v = static_cast<uint16_t*>(v_out);
+  a.out_length = out_length;
+  a.out_offset = out_offset;
+  return dispatch<false>(heads_per_group(num_heads, false, FLK_QK_HPG), batch, scale_is_f32,
+                         static_cast<hipStream_t>(stream), a);
+}
 
-  // Two heads per 16-lane group measured best at the Klein shapes (6 loads in flight per lane
-  // and 2x more blocks than four heads per group).
-  int hpg = (num_heads % 2 == 0) ? 2 : (num_heads % 3 == 0) ? 3 : 1;
-  if (FLK_QK_HPG > 0 && num_heads % FLK_QK_HPG == 0) hpg = FLK_QK_HPG;
-  const dim3 grid((length + kTokensPerBlock - 1) / kTokensPerBlock, num_heads / hpg, batch);
-  const bool gain = q_gain != 1.0f;
-  auto* s = static_cast<hipStream_t>(stream);
-  auto* in = static_cast<const uint16_t*>(qkv);
-  auto* q = static_cast<uint16_t*>(q_out);
-  auto* k = static_cast<uint16_t*>(k_out);
-  auto* v = static_cast<uint16_t*>(v_out);
-  if (scale_is_f32) {
-    return gain ? launch<true, true>(hpg, grid, s, in, qkv_batch_stride, qkv_row_stride, cos, sin,
-                                     table_row_stride, q_scale, k_scale, q_gain, length, num_heads,
-                                     q, k, v, out_length, out_offset)
-                : launch<true, false>(hpg, grid, s, in, qkv_batch_stride, qkv_row_stride, cos, sin,
-                                      table_row_stride, q_scale, k_scale, q_gain, length, num_heads,
-                                      q, k, v, out_length, out_offset);
-  }
-  return gain ? launch<false, true>(hpg, grid, s, in, qkv_batch_stride, qkv_row_stride, cos, sin,
-                                    table_row_stride, q_scale, k_scale, q_gain, length, num_heads,
-                                    q, k, v, out_length, out_offset)
-              : launch<false, false>(hpg, grid, s, in, qkv_batch_stride, qkv_row_stride, cos, sin,
-                                     table_row_stride, q_scale, k_scale, q_gain, length, num_heads,
-                                     q, k, v, out_length, out_offset);
+extern "C" int flk_qk_prep_ids(const void* qkv, int64_t qkv_batch_stride, int64_t qkv_row_stride,
+                               const float* ids, int64_t ids_row_stride, int n_axes,
+                               const int* axes_dim, float theta, const void* q_scale,
+                               const void* k_scale, int scale_is_f32, float q_gain, int batch,
+                               int length, int num_heads, int head_dim, void* q_out, void* k_out,
+                               void* v_out, int64_t out_length, int64_t out_offset, void* stream) {
+  const int st = check_common(qkv, qkv_batch_stride, qkv_row_stride, q_scale, k_scale, batch,
+                              length, num_heads, head_dim, q_out, k_out, v_out, out_length, out_offset);
+  Launch a{};
+  const int ax_st = flk_make_axes(n_axes, axes_dim, a.rope.ax);
+  if (ax_st != FLK_OK) return ax_st;
+  if (2 * a.rope.ax.first_pair[n_axes] != kHeadDim || ids_row_stride < n_axes) return FLK_E_INVALID;
+  if (st != FLK_OK) return st == kEmpty ? FLK_OK : st;
+  if (!ids) return FLK_E_INVALID;
+  if (!flk_host_aligned(ids, 4)) return FLK_E_ALIGN;
+  a.qkv = static_cast<const uint16_t*>(qkv);
+  a.batch_stride = qkv_batch_stride;
+  a.row_stride = qkv_row_stride;
+  a.rope.ids = ids;
+  a.rope.ids_stride = ids_row_stride;
+  a.rope.theta = theta;
+  a.q_scale = q_scale;
+  a.k_scale = k_scale;
+  a.q_gain = q_gain;
+  a.length = length;
+  a.num_heads = num_heads;
+  a.q = static_cast<uint16_t*>(q_out);
+  a.k = static_cast<uint16_t*>(k_out);
+  a.v = static_cast<uint16_t*>(v_out);
+  a.out_length = out_length;
+  a.out_offset = out_offset;
+  return dispatch<true>(heads_per_group(num_heads, true, FLK_QK_IDS_HPG), batch, scale_is_f32,
+                        static_cast<hipStream_t>(stream), a);
 }

@@ -1,39 +1,21 @@
 // RoPE tables on the GPU: rope.embed_nd (src/flicker/rope.py:9-21), kernels.lane_pair
-// (src/flicker/kernels.py:28-31) and the two fused.
-//
-// For pair k of an axis of width dim (k < dim/2) and position x:
-//   omega = 1 / theta^(2k/dim)   (f32: 2k/dim divided in f32, powf, 1/x)
-//   angle = x * omega            (f32)
-//   pe    = [[cos, -sin], [sin, cos]](angle)
-// Pairs of the axes are concatenated in axis order.  Each thread produces one
-// (token, pair) entry; the tables are built once per forward, not per block.
+// (src/flicker/kernels.py:28-31) and the two fused.  The angle arithmetic lives in
+// rope_math.h.  Each thread produces one (token, pair) entry; the tables are built once
+// per forward, not per block.
 
-#include "common.h"
+#include "rope_math.h"
 
 namespace {
 
-constexpr int kMaxAxes = 8;
+using flk::Axes;
 constexpr int kThreads = 256;
-
-struct Axes {
-  int count;
-  int dim[kMaxAxes];
-  int first_pair[kMaxAxes + 1];  // prefix sums of dim/2
-};
 
 __device__ __forceinline__ void angle_of(const float* __restrict__ ids, int64_t stride,
                                          int64_t t, int pair, const Axes& ax, float theta,
                                          float& c, float& s) {
-  int a = 0;
-#pragma unroll
-  for (int i = 1; i < kMaxAxes; ++i)
-    if (i < ax.count && pair >= ax.first_pair[i]) a = i;
-  const int kk = pair - ax.first_pair[a];
-  const float scale = (float)(2 * kk) / (float)ax.dim[a];
-  const float omega = 1.0f / powf(theta, scale);
-  const float angle = ids[t * stride + a] * omega;
-  c = cosf(angle);
-  s = sinf(angle);
+  int a;
+  const float omega = flk::pair_omega(pair, ax, theta, a);
+  flk::pair_cos_sin(ids[t * stride + a], omega, c, s);
 }
 
 __global__ __launch_bounds__(kThreads) void rope_embed_kernel(const float* __restrict__ ids,
@@ -77,20 +59,6 @@ __global__ __launch_bounds__(kThreads) void rope_lanes_kernel(const float* __res
   reinterpret_cast<float2*>(sin_t)[idx] = make_float2(-s, s);
 }
 
-int make_axes(int n_axes, const int* axes_dim, Axes& ax) {
-  if (n_axes < 1 || n_axes > kMaxAxes || !axes_dim) return FLK_E_INVALID;
-  ax.count = n_axes;
-  ax.first_pair[0] = 0;
-  for (int i = 0; i < kMaxAxes; ++i) ax.dim[i] = 2;
-  for (int i = 0; i < n_axes; ++i) {
-    if (axes_dim[i] <= 0 || axes_dim[i] % 2) return FLK_E_INVALID;
-    ax.dim[i] = axes_dim[i];
-    ax.first_pair[i + 1] = ax.first_pair[i] + axes_dim[i] / 2;
-  }
-  for (int i = n_axes + 1; i <= kMaxAxes; ++i) ax.first_pair[i] = ax.first_pair[n_axes];
-  return FLK_OK;
-}
-
 unsigned blocks_for(int64_t n) { return (unsigned)((n + kThreads - 1) / kThreads); }
 
 }  // namespace
@@ -99,7 +67,7 @@ extern "C" int flk_rope_embed(const float* ids, int64_t ids_row_stride, int64_t 
                               int n_axes, const int* axes_dim, float theta, float* pe,
                               void* stream) {
   Axes ax;
-  const int st = make_axes(n_axes, axes_dim, ax);
+  const int st = flk_make_axes(n_axes, axes_dim, ax);
   if (st != FLK_OK) return st;
   if (length < 0 || ids_row_stride < n_axes) return FLK_E_INVALID;
   const int64_t n = length * ax.first_pair[n_axes];
@@ -130,7 +98,7 @@ extern "C" int flk_rope_lanes(const float* ids, int64_t ids_row_stride, int64_t 
                               int n_axes, const int* axes_dim, float theta, float* cos,
                               float* sin, void* stream) {
   Axes ax;
-  const int st = make_axes(n_axes, axes_dim, ax);
+  const int st = flk_make_axes(n_axes, axes_dim, ax);
   if (st != FLK_OK) return st;
   if (length < 0 || ids_row_stride < n_axes) return FLK_E_INVALID;
   const int64_t n = length * ax.first_pair[n_axes];

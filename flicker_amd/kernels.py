@@ -12,7 +12,9 @@ tensors on an MI355X; every computation runs in the HIP kernels of libflicker_hi
 Beyond the reference, ``qk_prep`` takes optional ``out=(q, k, v)`` / ``out_offset`` so
 the text and image streams of a double block can be written straight into one
 concatenated buffer, and it accepts a strided ``qkv`` view (e.g. the qkv part of a
-single block's fused linear1 output) without a copy.
+single block's fused linear1 output) without a copy.  In place of ``Freqs`` it also
+accepts ``PositionIds``: the kernel then computes the RoPE lanes from the position ids
+(rope.py:9-21 + kernels.py:28-31, -> flk_qk_prep_ids) instead of reading two f32 tables.
 """
 
 from __future__ import annotations
@@ -33,6 +35,18 @@ class Freqs(NamedTuple):
     cos: torch.Tensor
     sin: torch.Tensor
     q_gain: float = 1.0
+
+
+class PositionIds(NamedTuple):
+    """Position ids (L, n_axes) float32 on the GPU and the RoPE constants from which qk_prep
+    computes its cos / sin lanes in-kernel; the values equal ``rope.rope_lanes(ids, q_gain,
+    axes_dim, theta)`` bit for bit.  Defaults are Klein 4B's (config.py:36: four axes of 32,
+    theta 2000)."""
+
+    ids: torch.Tensor
+    q_gain: float = 1.0
+    axes_dim: tuple = (32, 32, 32, 32)
+    theta: float = 2000.0
 
 
 EPS = 1e-6
@@ -79,7 +93,36 @@ def lane_pair(freqs: torch.Tensor, q_gain: float = 1.0) -> Freqs:
     return Freqs(cos, sin, float(q_gain))
 
 
-def _launch_qk_prep(qkv, q_scale, k_scale, freqs: Freqs, num_heads: int, out, out_offset: int):
+def _table_args(freqs: Freqs, length: int, head_dim: int):
+    cos, sin, _ = freqs
+    for name, t in (("freqs.cos", cos), ("freqs.sin", sin)):
+        _on_gpu(name, t)
+    if cos.shape != (length, head_dim) or sin.shape != (length, head_dim):
+        raise ValueError(f"freqs tables must be ({length}, {head_dim}), got {tuple(cos.shape)} / {tuple(sin.shape)}")
+    if cos.dtype != torch.float32 or sin.dtype != torch.float32:
+        raise TypeError("freqs.cos / freqs.sin must be float32")
+    cos = cos if cos.stride(1) == 1 and cos.stride(0) % 4 == 0 and cos.data_ptr() % 16 == 0 else cos.contiguous()
+    sin = sin if sin.stride(1) == 1 and sin.stride(0) % 4 == 0 and sin.data_ptr() % 16 == 0 else sin.contiguous()
+    if sin.stride(0) != cos.stride(0):
+        cos, sin = cos.contiguous(), sin.contiguous()
+    return cos, sin
+
+
+def _id_args(pos: PositionIds, length: int, head_dim: int):
+    ids = pos.ids
+    _on_gpu("ids", ids)
+    if ids.dim() == 3:
+        ids = ids[0]   # batch 0, as lane_pair takes (kernels.py:30)
+    if ids.dim() != 2 or ids.shape[0] != length or ids.shape[1] != len(pos.axes_dim):
+        raise ValueError(f"ids must be ({length}, {len(pos.axes_dim)}), got {tuple(pos.ids.shape)}")
+    if ids.dtype != torch.float32:
+        raise TypeError(f"ids must be float32, got {ids.dtype}")
+    if sum(pos.axes_dim) != head_dim:
+        raise ValueError(f"axes_dim {tuple(pos.axes_dim)} must sum to head_dim {head_dim}")
+    return ids if ids.stride(1) == 1 else ids.contiguous()
+
+
+def _launch_qk_prep(qkv, q_scale, k_scale, freqs, num_heads: int, out, out_offset: int):
     batch, length, width = qkv.shape
     head_dim = width // (3 * num_heads)
     if 3 * num_heads * head_dim != width:
@@ -88,22 +131,21 @@ def _launch_qk_prep(qkv, q_scale, k_scale, freqs: Freqs, num_heads: int, out, ou
         raise ValueError(f"qk_prep: head_dim {head_dim} unsupported (kernels are built for {HEAD_DIM})")
     if qkv.dtype != torch.bfloat16:
         raise TypeError(f"qkv must be bfloat16, got {qkv.dtype}")
-    cos, sin, q_gain = freqs
-    for name, t in (("freqs.cos", cos), ("freqs.sin", sin), ("q_scale", q_scale), ("k_scale", k_scale)):
+    if isinstance(freqs, PositionIds):
+        rope = _id_args(freqs, length, head_dim)
+    elif isinstance(freqs, Freqs) or (isinstance(freqs, tuple) and len(freqs) == 3):
+        freqs = Freqs(*freqs)
+        rope = _table_args(freqs, length, head_dim)
+    else:
+        raise TypeError(f"freqs must be Freqs or PositionIds, got {type(freqs).__name__}")
+    q_gain = freqs.q_gain
+    for name, t in (("q_scale", q_scale), ("k_scale", k_scale)):
         _on_gpu(name, t)
-    if cos.shape != (length, head_dim) or sin.shape != (length, head_dim):
-        raise ValueError(f"freqs tables must be ({length}, {head_dim}), got {tuple(cos.shape)} / {tuple(sin.shape)}")
-    if cos.dtype != torch.float32 or sin.dtype != torch.float32:
-        raise TypeError("freqs.cos / freqs.sin must be float32")
     if q_scale.numel() != head_dim or k_scale.numel() != head_dim:
         raise ValueError(f"q_scale / k_scale must hold {head_dim} values")
     if q_scale.dtype != k_scale.dtype or q_scale.dtype not in (torch.bfloat16, torch.float32):
         raise TypeError("q_scale and k_scale must share one dtype, bfloat16 or float32")
     qkv = _dense_rows(qkv)
-    cos = cos if cos.stride(1) == 1 and cos.stride(0) % 4 == 0 and cos.data_ptr() % 16 == 0 else cos.contiguous()
-    sin = sin if sin.stride(1) == 1 and sin.stride(0) % 4 == 0 and sin.data_ptr() % 16 == 0 else sin.contiguous()
-    if sin.stride(0) != cos.stride(0):
-        cos, sin = cos.contiguous(), sin.contiguous()
     q_scale = q_scale.reshape(-1).contiguous()
     k_scale = k_scale.reshape(-1).contiguous()
 
@@ -126,21 +168,31 @@ def _launch_qk_prep(qkv, q_scale, k_scale, freqs: Freqs, num_heads: int, out, ou
         if out_offset < 0 or out_offset + length > out_length:
             raise ValueError(f"out_offset {out_offset} + L {length} exceeds the output length {out_length}")
 
-    status = _lib.lib().flk_qk_prep(
-        qkv.data_ptr(), qkv.stride(0), qkv.stride(1), cos.data_ptr(), sin.data_ptr(), cos.stride(0),
-        q_scale.data_ptr(), k_scale.data_ptr(), int(q_scale.dtype == torch.float32), float(q_gain),
-        batch, length, num_heads, head_dim, out[0].data_ptr(), out[1].data_ptr(), out[2].data_ptr(),
-        out_length, out_offset, _lib.stream_of(qkv))
-    _lib.check(status, "flk_qk_prep")
+    common = (q_scale.data_ptr(), k_scale.data_ptr(), int(q_scale.dtype == torch.float32), float(q_gain),
+              batch, length, num_heads, head_dim, out[0].data_ptr(), out[1].data_ptr(), out[2].data_ptr(),
+              out_length, out_offset, _lib.stream_of(qkv))
+    if isinstance(freqs, PositionIds):
+        status = _lib.lib().flk_qk_prep_ids(
+            qkv.data_ptr(), qkv.stride(0), qkv.stride(1), rope.data_ptr(), rope.stride(0),
+            len(freqs.axes_dim), _lib.int_array(freqs.axes_dim), float(freqs.theta), *common)
+        _lib.check(status, "flk_qk_prep_ids")
+    else:
+        cos, sin = rope
+        status = _lib.lib().flk_qk_prep(
+            qkv.data_ptr(), qkv.stride(0), qkv.stride(1), cos.data_ptr(), sin.data_ptr(), cos.stride(0),
+            *common)
+        _lib.check(status, "flk_qk_prep")
     return out
 
 
-def qk_prep(qkv: torch.Tensor, q_scale: torch.Tensor, k_scale: torch.Tensor, freqs: Freqs,
-            num_heads: int, *, rows: int | None = None, interpret: bool = False,
+def qk_prep(qkv: torch.Tensor, q_scale: torch.Tensor, k_scale: torch.Tensor,
+            freqs: Freqs | PositionIds, num_heads: int, *, rows: int | None = None,
+            interpret: bool = False,
             out=None, out_offset: int = 0):
     """kernels.py:57-91 -- fused head transpose + QK-RMSNorm + RoPE (+ q_gain on q).
 
-    qkv (B, L, 3*H*D) bf16 -> q, k, v (B, H, L, D) bf16.  As in the reference, ``rows``
+    qkv (B, L, 3*H*D) bf16 -> q, k, v (B, H, L, D) bf16.  ``freqs`` is a Freqs (lane
+    tables) or a PositionIds (lanes computed in-kernel, same values).  As in the reference, ``rows``
     (or the default row tile) must divide L; the HIP kernel itself tiles by 16 tokens."""
     if interpret:
         raise ValueError("interpret=True is Pallas' CPU emulation; flicker_amd has one HIP path")

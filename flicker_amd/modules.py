@@ -12,7 +12,7 @@ from __future__ import annotations
 
 import torch
 
-from .kernels import Freqs, _launch_qk_prep, attend_merged, lane_pair
+from .kernels import Freqs, PositionIds, _launch_qk_prep, attend_merged, lane_pair
 
 
 def heads(qkv: torch.Tensor, num_heads: int):
@@ -29,7 +29,7 @@ def merge_heads(x: torch.Tensor) -> torch.Tensor:
     return x.transpose(1, 2).reshape(b, n, h * d)
 
 
-def qkv_prep(qkv, q_scale, k_scale, pe, freqs: Freqs | None, num_heads: int, *, out=None,
+def qkv_prep(qkv, q_scale, k_scale, pe, freqs: Freqs | PositionIds | None, num_heads: int, *, out=None,
              out_offset: int = 0):
     """modules.py:68-80 -- QK-RMSNorm + RoPE + head split.  The reference switches between its
     fused kernel and a plain-XLA branch; here both are the one HIP kernel: without ``freqs``
@@ -40,11 +40,16 @@ def qkv_prep(qkv, q_scale, k_scale, pe, freqs: Freqs | None, num_heads: int, *, 
     return _launch_qk_prep(qkv, q_scale, k_scale, freqs, num_heads, out, out_offset)
 
 
-def _slice(freqs: Freqs, start: int, stop: int) -> Freqs:
+def _slice(freqs, start: int, stop: int):
+    """Rows start:stop of the RoPE source of the joint sequence (tables or position ids)."""
+    if isinstance(freqs, PositionIds):
+        ids = freqs.ids[0] if freqs.ids.dim() == 3 else freqs.ids
+        return freqs._replace(ids=ids[start:stop])
     return Freqs(freqs.cos[start:stop], freqs.sin[start:stop], freqs.q_gain)
 
 
-def double_attention(txt_qkv, img_qkv, txt_scales, img_scales, freqs: Freqs, num_heads: int):
+def double_attention(txt_qkv, img_qkv, txt_scales, img_scales, freqs: Freqs | PositionIds,
+                     num_heads: int):
     """modules.py:127-139 + 157-158 -- per-stream qk prep, joint text|image attention, merge,
     split back into (txt_attn, img_attn), each (B, L_stream, H*D).
 
@@ -62,7 +67,8 @@ def double_attention(txt_qkv, img_qkv, txt_scales, img_scales, freqs: Freqs, num
     return attn[:, :num_txt], attn[:, num_txt:]
 
 
-def single_attention(linear1_out, q_scale, k_scale, freqs: Freqs, num_heads: int, hidden: int):
+def single_attention(linear1_out, q_scale, k_scale, freqs: Freqs | PositionIds, num_heads: int,
+                     hidden: int):
     """modules.py:185-191 + 198 -- the qkv part of the fused linear1 output (a strided view,
     consumed without a copy) -> qk prep -> attention -> merge; returns (attn, mlp)."""
     qkv, mlp = linear1_out[..., : 3 * hidden], linear1_out[..., 3 * hidden:]

@@ -5,6 +5,7 @@ are built on the GPU by libflicker_hip.so:
 
   rope_freqs / embed_nd   rope.py:9-21     -> flk_rope_embed  ((..., L, P, 2, 2) rotation matrices)
   rope_lanes              embed_nd + kernels.lane_pair in one pass -> flk_rope_lanes
+  position_ids            no table at all: qk_prep computes the lanes in-kernel -> flk_qk_prep_ids
 """
 
 from __future__ import annotations
@@ -14,7 +15,7 @@ import torch
 
 from . import _lib
 from .config import Klein4B
-from .kernels import Freqs
+from .kernels import Freqs, PositionIds
 
 _KLEIN = Klein4B()
 
@@ -88,3 +89,16 @@ def rope_lanes(ids, q_gain: float = 1.0, axes_dim=_KLEIN.axes_dim, theta: float 
                                          float(theta), cos.data_ptr(), sin.data_ptr(), _lib.stream_of(cos)),
                "flk_rope_lanes")
     return Freqs(cos, sin, float(q_gain))
+
+
+def position_ids(ids, q_gain: float = 1.0, axes_dim=_KLEIN.axes_dim, theta: float = _KLEIN.theta,
+                 device=None) -> PositionIds:
+    """The table-free RoPE source for qk_prep: ids (L, A) on the GPU plus the constants.
+    qk_prep(..., position_ids(ids, g), ...) equals qk_prep(..., rope_lanes(ids, g), ...)
+    bit for bit, without building or reading the two (L, sum(axes)) float32 tables."""
+    ids = _ids_on(ids, device)
+    if ids.dim() == 3:
+        ids = ids[0]
+    if ids.dim() != 2 or ids.shape[1] != len(axes_dim):
+        raise ValueError(f"ids must be (L, {len(axes_dim)}), got {tuple(ids.shape)}")
+    return PositionIds(ids, float(q_gain), tuple(int(a) for a in axes_dim), float(theta))

@@ -49,11 +49,13 @@ class Workload:
     def qkv_width(self) -> int:
         return 3 * self.num_heads * self.head_dim
 
-    def qk_prep_bytes(self) -> int:
-        """Algorithmic HBM bytes of one qk_prep: read QKV + write Q, K, V (bf16), read the
-        float32 cos/sin tables once and the two bf16 scale vectors."""
+    def qk_prep_bytes(self, tables: bool = True) -> int:
+        """Algorithmic HBM bytes of one qk_prep: read QKV + write Q, K, V (bf16), the two bf16
+        scale vectors, and either the float32 cos/sin tables (read once) or, for the variant
+        that computes the lanes from position ids, the (L, 4) float32 ids."""
         act = self.batch * self.length * self.qkv_width * 2
-        return 2 * act + 2 * self.length * self.head_dim * 4 + 2 * self.head_dim * 2
+        rope = 2 * self.length * self.head_dim * 4 if tables else self.length * 4 * 4
+        return 2 * act + rope + 2 * self.head_dim * 2
 
     def attend_flops(self) -> int:
         """4 B H L^2 D: the QK^T and PV products of non-causal attention (exp and sums not counted)."""

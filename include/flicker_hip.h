@@ -54,6 +54,25 @@ int flk_qk_prep(const void* qkv, int64_t qkv_batch_stride, int64_t qkv_row_strid
                 void* stream);
 
 /*
+ * flk_qk_prep with the RoPE lanes computed in the kernel from position ids instead of read
+ * from cos / sin tables: the fused form of qk_prep(qkv, ..., lane_pair(embed_nd(ids))),
+ * i.e. kernels.qk_prep (src/flicker/kernels.py:57-91) over rope.embed_nd
+ * (src/flicker/rope.py:9-21) and kernels.lane_pair (kernels.py:28-31).  The cos / sin values
+ * are bit-identical to those flk_rope_lanes stores, so the outputs equal flk_qk_prep's with
+ * those tables; the two (length, head_dim) f32 tables are neither built nor read.
+ *   ids        (length, n_axes) float32 positions, row t at t*ids_row_stride floats; shared
+ *              by every batch element (lane_pair takes batch 0)
+ *   n_axes, axes_dim, theta  as flk_rope_lanes; sum(axes_dim) must equal head_dim
+ * Every other argument as flk_qk_prep.
+ */
+int flk_qk_prep_ids(const void* qkv, int64_t qkv_batch_stride, int64_t qkv_row_stride,
+                    const float* ids, int64_t ids_row_stride, int n_axes, const int* axes_dim,
+                    float theta, const void* q_scale, const void* k_scale, int scale_is_f32,
+                    float q_gain, int batch, int length, int num_heads, int head_dim,
+                    void* q_out, void* k_out, void* v_out, int64_t out_length,
+                    int64_t out_offset, void* stream);
+
+/*
  * Bounded flash attention: softmax without the running max, legal because the
  * QK-norm scales bound every logit (checked at load time, kernels.logit_bound).
  * Replaces kernels.attend (src/flicker/kernels.py:105-145).

@@ -155,3 +155,67 @@ def test_qk_prep_klein_1024_full(device):
     torch.cuda.synchronize()
     check_qkv("klein_1024", got, P.qk_prep_fused(to_np(qkv), to_np(qs), to_np(ks), tables, 24,
                                                   return_normed=True), tables.q_gain)
+
+
+def _ids_and_tables_paths(device, qkv, qs, ks, ids, heads, gain):
+    """qk_prep through position ids (cos/sin in-kernel) and through rope_lanes tables; also
+    returns those tables (whose agreement with the oracle's is test_gpu_rope's)."""
+    from flicker_amd import rope
+    ids_dev = torch.from_numpy(np.ascontiguousarray(ids, dtype=np.float32)).to(device)
+    args = (qkv.to(device), qs.to(device), ks.to(device))
+    freqs = rope.rope_lanes(ids_dev, gain)
+    via_ids = modules.qkv_prep(*args, None, rope.position_ids(ids_dev, gain), heads)
+    via_tables = modules.qkv_prep(*args, None, freqs, heads)
+    torch.cuda.synchronize()
+    return via_ids, via_tables, P.Freqs(to_np(freqs.cos), to_np(freqs.sin), gain)
+
+
+@pytest.mark.parametrize("batch,length,heads,gain", [
+    (1, 64, 24, 1 / math.sqrt(128)),
+    (2, 100, 24, 1.0),
+    (1, 1536, 6, 0.5),
+    (1, 17, 5, 1 / math.sqrt(128)),
+    (3, 256, 3, 1 / math.sqrt(128)),
+])
+def test_qk_prep_ids_equals_table_path(device, batch, length, heads, gain):
+    """flk_qk_prep_ids computes the same cos/sin bits as flk_rope_lanes, so the outputs are
+    identical to the table path's; against the oracle fed those same lane values, the usual
+    qk_prep gate.  (With the oracle's own numpy tables, f32 cos/sin one ulp apart flip a few
+    bf16 output roundings -- within the per-element bound, but not an exact-table count.)"""
+    qkv, qs, ks, ids = make_case(batch, length, heads, seed=100 + length + heads)
+    via_ids, via_tables, lanes = _ids_and_tables_paths(device, qkv, qs, ks, ids, heads, gain)
+    for name, a, b in zip("qkv", via_ids, via_tables):
+        assert torch.equal(a, b), f"{name}: ids path differs from the table path"
+    want = P.qk_prep_fused(to_np(qkv), to_np(qs), to_np(ks), lanes, heads, return_normed=True)
+    check_qkv(f"ids B{batch} L{length} H{heads}", via_ids, want, gain)
+
+
+@pytest.mark.parametrize("name", ["klein_1024", "klein_2048"])
+def test_qk_prep_ids_klein_positions(device, name):
+    """The workloads' real text|image ids (text positions up to 511, image rows/cols up to 127
+    at 2048^2) through both RoPE sources; two heads keep the 2048^2 case small."""
+    from flicker_amd import workloads
+    w = workloads.WORKLOADS[name]
+    ids = workloads.make_ids(w)
+    length, heads = ids.shape[0], 2
+    g = torch.Generator().manual_seed(5)
+    qkv = torch.randn(1, length, 3 * heads * D, generator=g).to(torch.bfloat16)
+    qs, ks = workloads.make_scales(w)
+    via_ids, via_tables, _ = _ids_and_tables_paths(device, qkv, qs, ks, ids, heads, workloads.q_gain(w))
+    for n, a, b in zip("qkv", via_ids, via_tables):
+        assert torch.equal(a, b), f"{name} {n}: ids path differs from the table path"
+
+
+def test_double_attention_with_position_ids(device):
+    """A double block's attention section is identical with ids or tables as the RoPE source."""
+    from flicker_amd import rope
+    heads, n_txt, n_img = 24, 512, 256
+    txt, qs_t, ks_t, _ = make_case(1, n_txt, heads, seed=31)
+    img, qs_i, ks_i, _ = make_case(1, n_img, heads, seed=32)
+    ids = torch.from_numpy(rope.sequence_ids(n_txt, 16, 16)).to(device)
+    dev = lambda *ts: tuple(t.to(device) for t in ts)  # noqa: E731
+    out = []
+    for src in (rope.position_ids(ids, 1 / math.sqrt(128)), rope.rope_lanes(ids, 1 / math.sqrt(128))):
+        out.append(modules.double_attention(*dev(txt, img), dev(qs_t, ks_t), dev(qs_i, ks_i), src, heads))
+    torch.cuda.synchronize()
+    assert torch.equal(out[0][0], out[1][0]) and torch.equal(out[0][1], out[1][1])

@@ -81,6 +81,38 @@ def test_qk_prep_validation(lib):
     assert call(l=0) == _lib.FLK_OK
 
 
+def test_qk_prep_ids_validation(lib):
+    f = lib.flk_qk_prep_ids
+    args = dict(qkv=FAKE, bs=4608 * 9216, rs=9216, ids=FAKE, ids_rs=4, n_axes=4,
+                axes=_lib.int_array([32, 32, 32, 32]), theta=2000.0, qs=FAKE, ks=FAKE, f32=0, gain=1.0,
+                b=1, l=4608, h=24, d=128, q=FAKE, k=FAKE, v=FAKE, ol=4608, oo=0, st=None)
+
+    def call(**kw):
+        a = dict(args, **kw)
+        return f(*a.values())
+
+    assert call(d=64) == _lib.FLK_E_UNSUPPORTED
+    assert call(axes=_lib.int_array([32, 32, 32, 30])) == _lib.FLK_E_INVALID   # sum != head_dim
+    assert call(axes=_lib.int_array([32, 32, 32, 31])) == _lib.FLK_E_INVALID   # odd axis
+    assert call(n_axes=9) == _lib.FLK_E_INVALID
+    assert call(ids_rs=3) == _lib.FLK_E_INVALID                                # row shorter than n_axes
+    assert call(ids=None) == _lib.FLK_E_INVALID
+    assert call(ids=FAKE + 2) == _lib.FLK_E_ALIGN
+    assert call(oo=1) == _lib.FLK_E_INVALID
+    assert call(rs=9220) == _lib.FLK_E_ALIGN
+    assert call(l=0) == _lib.FLK_OK
+    assert call(l=0, ids=None, qkv=None) == _lib.FLK_OK                       # empty: nothing is read
+
+
+def test_position_ids_python_errors():
+    pos = kernels.PositionIds(torch.zeros(8, 4), 1.0)
+    qkv = torch.zeros(1, 8, 3 * 24 * 128, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="GPU only"):
+        kernels._launch_qk_prep(qkv, torch.ones(128), torch.ones(128), pos, 24, None, 0)
+    with pytest.raises(TypeError, match="Freqs or PositionIds"):
+        kernels._launch_qk_prep(qkv, torch.ones(128), torch.ones(128), object(), 24, None, 0)
+
+
 def test_rope_validation(lib):
     axes = _lib.int_array([32, 32, 32, 31])
     assert lib.flk_rope_lanes(FAKE, 4, 10, 4, axes, 2000.0, FAKE, FAKE, None) == _lib.FLK_E_INVALID
