@@ -127,9 +127,11 @@ def test_quantize_act_bit_exact(device, strided):
     assert host(a)[17] == 1.0
 
 
-@pytest.mark.parametrize("m,k,n", [(300, 256, 520), (1, 128, 4), (257, 3072, 260), (512, 128, 1024), (4608, 3072, 9216 // 36)])
+@pytest.mark.parametrize("m,k,n", [(300, 256, 520), (1, 128, 4), (257, 3072, 260), (512, 128, 1024),
+                                   (4608, 3072, 9216 // 36), (2600, 384, 6000)])
 def test_gemm_tails_bit_exact(device, m, k, n):
-    """Ragged tiles in both output dimensions; full-range int8 operands."""
+    """Ragged tiles in both output dimensions; full-range int8 operands.  The last case has
+    11 x 24 = 264 tiles, more than one per CU, so blocks walk several tiles, ragged ones included."""
     rng = np.random.default_rng(m * 7 + n)
     xq = rng.integers(-127, 128, (m, k), dtype=np.int8)
     wq = rng.integers(-127, 128, (k, n), dtype=np.int8)
