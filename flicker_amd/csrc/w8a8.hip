@@ -57,6 +57,19 @@ __device__ __forceinline__ int quantize(float v, float scale) {
   return (int)fminf(fmaxf(q, -kQMax), kQMax);
 }
 
+// quantize(v, scale) without a division per element.  r = 1/scale is rounded once per row;
+// p = v * r is then within 3 * 2^-24 |p| < 2^-22 |p| of the correctly rounded quotient q
+// (r, p and q each carry at most half an ulp of relative error).  When p is farther than
+// 2^-21 |p| from a rounding boundary (a half-integer), q lies on the same side and
+// rint(p) == rint(q); otherwise -- p near a tie, or not finite -- the division is done.
+// p - rint(p) is exact (Sterbenz), so the test itself does not round.
+__device__ __forceinline__ int quantize_recip(float v, float scale, float r) {
+  const float p = v * r;
+  float t = __builtin_rintf(p);
+  if (!(fabsf(p - t) < 0.5f - fabsf(p) * 0x1p-21f)) t = __builtin_rintf(v / scale);
+  return (int)fminf(fmaxf(t, -kQMax), kQMax);
+}
+
 __device__ __forceinline__ uint32_t pack_i8x4(int a, int b, int c, int d) {
   return (uint32_t)(a & 0xFF) | ((uint32_t)(b & 0xFF) << 8) | ((uint32_t)(c & 0xFF) << 16) |
          ((uint32_t)(d & 0xFF) << 24);
@@ -300,14 +313,16 @@ __global__ __launch_bounds__(256) void quantize_act_kernel(const uint16_t* __res
     }
   }
   const float a = absmax_scale(wave_max(amax));
+  const float ra = 1.0f / a;
   int8_t* dst = xq + (int64_t)row * K;
 #pragma unroll
   for (int c = 0; c < kChunks; ++c) {
     const int idx = c * 64 + lane;
     if (idx < nch) {
+      auto qz = [&](float v) { return quantize_recip(v, a, ra); };
       uint2 packed;
-      packed.x = pack_i8x4(quantize(xh[c][0], a), quantize(xh[c][1], a), quantize(xh[c][2], a), quantize(xh[c][3], a));
-      packed.y = pack_i8x4(quantize(xh[c][4], a), quantize(xh[c][5], a), quantize(xh[c][6], a), quantize(xh[c][7], a));
+      packed.x = pack_i8x4(qz(xh[c][0]), qz(xh[c][1]), qz(xh[c][2]), qz(xh[c][3]));
+      packed.y = pack_i8x4(qz(xh[c][4]), qz(xh[c][5]), qz(xh[c][6]), qz(xh[c][7]));
       reinterpret_cast<uint2*>(dst)[idx] = packed;
     }
   }

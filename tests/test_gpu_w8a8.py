@@ -127,6 +127,26 @@ def test_quantize_act_bit_exact(device, strided):
     assert host(a)[17] == 1.0
 
 
+def test_quantize_act_near_ties(device):
+    """Rows whose quotients sit next to half-integers (v = amax / 2 -> v / a ~ 63.5), where a
+    reciprocal multiply rounds differently from the division: the kernel's fast path must
+    hand these to the division.  Each row also holds random values below its amax."""
+    from tests.test_oracle_pins import NEAR_TIE_ROWS
+    rng = np.random.default_rng(17)
+    k = 512
+    rows = []
+    for amax in NEAR_TIE_ROWS:
+        r = rng.uniform(-amax, amax, k).astype(np.float32)
+        r[0], r[1], r[2] = amax, amax / 2, -amax / 2
+        rows.append(r)
+    x = torch.from_numpy(np.stack(rows)).to(torch.bfloat16)
+    inv = np.ones(k, np.float32)
+    xq, a = w8a8.quantize_act(x.to(device), torch.from_numpy(inv).to(device))
+    xq_want, a_want = Q.quantize_act(x.float().numpy(), inv)
+    np.testing.assert_array_equal(host(a), a_want)
+    np.testing.assert_array_equal(host(xq), xq_want)
+
+
 @pytest.mark.parametrize("m,k,n", [(300, 256, 520), (1, 128, 4), (257, 3072, 260), (512, 128, 1024),
                                    (4608, 3072, 9216 // 36), (2600, 384, 6000)])
 def test_gemm_tails_bit_exact(device, m, k, n):

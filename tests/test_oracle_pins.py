@@ -345,3 +345,33 @@ def test_modulate_known_answers():
         one = bf16_round(np.float32(1.0) + np.float32(scale[b, j]))
         want = bf16_round(np.float32(bf16_round(np.float32(one * base[b, t, j])) + np.float32(shift[b, j])))
         assert got[b, t, j] == want
+
+
+# Rows whose quotient v / a lands next to a half-integer: a = fl(amax / 127), v = amax / 2, so
+# v / a is within an ulp of 63.5.  Found by exhaustive search over bf16 v for these amax.
+NEAR_TIE_ROWS = (2.359375, 108.0, 144.0, 53.25, 422.0)
+
+
+def _exact_f32_quotient_rint(v: float, a: float) -> int:
+    """rint of the correctly rounded f32 quotient, from exact rationals (no float division)."""
+    from fractions import Fraction
+    z = Fraction(v) / Fraction(a)
+    lo = np.float32(float(z))                      # nearest double, then nearest f32 ...
+    cands = [np.nextafter(lo, np.float32(-np.inf)), lo, np.nextafter(lo, np.float32(np.inf))]
+    q = min(cands, key=lambda c: (abs(Fraction(float(c)) - z), int(np.float32(c).view(np.int32)) & 1))
+    return int(np.rint(q))
+
+
+def test_quantize_near_ties_known_answers():
+    """The oracle quantises with the correctly rounded division: its codes equal the ones
+    derived from exact rationals, and a reciprocal multiply would give other codes."""
+    for amax in NEAR_TIE_ROWS:
+        v = np.float32(amax / 2)
+        x = np.zeros((1, 8), np.float32)
+        x[0, 0], x[0, 1] = amax, v
+        xq, a = Q.quantize_act(x, np.ones(8, np.float32))
+        assert a[0] == np.float32(np.float32(amax) / np.float32(127))
+        assert xq[0, 0] == 127
+        assert xq[0, 1] == _exact_f32_quotient_rint(float(v), float(a[0])), amax
+        recip = int(np.rint(np.float32(v * np.float32(np.float32(1) / a[0]))))
+        assert recip != xq[0, 1], f"amax {amax}: the vector does not separate division from reciprocal"
