@@ -23,14 +23,15 @@
 // GEMM.  A block of 8 waves (two per SIMD) owns a 256 (n) x 256 (m) output tile and
 // computes it transposed, Y^T = WqT . Xq^T, with v_mfma_i32_32x32x32_i8: A operand = 32 WqT
 // rows x 32 k bytes, B operand = 32 Xq rows x 32 k bytes, both one ds_read_b128 per lane.
-// In the 32x32 accumulator a lane owns one token and 4 x 4 consecutive output channels, so
-// the epilogue stores 4 bf16 (8 bytes) per register group.  Each wave holds a 128 (n) x 64
-// (m) sub-tile: 8 accumulators of 16 int32 (128 registers), 6 operand reads per 8 MFMAs.
-// k advances in 64-byte stages through a 4-stage LDS ring filled by
-// global_load_lds_dwordx4 (no registers); stage rows are 64 bytes = 4 chunks of 16 B
-// stored at chunk ^ ((row >> 1) & 3), which keeps each 8-lane phase of an operand read
-// on distinct banks.  Blocks are renumbered so consecutive output tiles share an XCD
-// (and its L2), and grouped so that 4 token tiles sweep the channel tiles together.
+// In the 32x32 accumulator a lane owns one token and 4 x 4 consecutive output channels.
+// Each wave holds a 128 (n) x 64 (m) sub-tile: 8 accumulators of 16 int32 (128 registers),
+// 6 operand reads per 8 MFMAs.  k advances in 128-byte stages (one full 128-byte line per
+// operand row) through two 64 KiB LDS buffers filled by global_load_lds_dwordx4 (no
+// registers); a row's 16-byte chunk c is stored at c ^ gswz(row), which keeps the 8- and
+// 16-lane phases of an operand read on distinct banks.  The epilogue rescales into LDS and
+// stores whole 256-byte output rows.  Blocks are renumbered so consecutive output tiles
+// share an XCD (and its L2), and grouped so that 4 token tiles sweep the channel tiles
+// together.
 
 #include "qk_math.h"
 
