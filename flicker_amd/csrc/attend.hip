@@ -27,7 +27,7 @@
 // element n+2, exp of n+1, and on every second slot the bf16 pack of a pair); the row sum
 // of the unit's packed pairs follows the phase's last MFMA as one run of v_dot2.  At two
 // waves per SIMD that VALU load mostly hides under the matrix pipe.  Each MFMA's LDS
-// operand is read kLead slots ahead into a 4-deep register ring, and the packed P values
+// operand is read kLead slots ahead into an 8-deep register ring, and the packed P values
 // are tied to their slots so the compiler cannot batch them elsewhere.
 //
 // Staging.  K and V live in separate 4-deep rings of 64-key tiles (16 KiB each).
@@ -65,8 +65,11 @@ constexpr int kRowsPerWave = kBN / kWaves;     // tile rows each wave copies (8)
 constexpr int kDmaPerTensor = kRowsPerWave / 4;  // copy instructions per wave per tile (2)
 constexpr int kDmaPerIter = 2 * kDmaPerTensor;   // K and V
 constexpr int kXcds = 8;
-constexpr int kLead = 3;                 // slots between an operand's LDS read and its MFMA
-constexpr int kOpRing = 4;               // operand registers in flight (> kLead)
+constexpr int kLead = 4;                 // slots between an operand's LDS read and its MFMA
+constexpr int kOpRing = 8;               // operand registers in flight (> kLead)
+// Slot n of every phase uses ops[n % kOpRing], and the next phase's first operands are read
+// into the same places, so the ring must divide the 16 slots of a phase.
+static_assert(16 % kOpRing == 0 && kOpRing > kLead, "operand ring must divide 16 and exceed kLead");
 constexpr float kLog2e = 1.4426950408889634f;
 
 using flk::bf16x2;
