@@ -19,6 +19,10 @@ Counter runs (rocprofv3 --pmc) use --only to launch one kernel kind, and
 --ingest-pmc turns a FETCH_SIZE run and a WRITE_SIZE run of
 `--only calibrate` into the per-launch HBM traffic summary
 profiles/hbm_traffic_<workload>.json that the default run reports as roofline.traffic.
+--ingest-mfma turns one run with the MFMA counters (MFMA_COUNTERS) into
+profiles/mfma_util_<workload>.json: per dispatch of attend and of the int8 GEMM, the
+fraction of cycles the matrix pipe is busy and the shader clock the kernel ran at, which the
+default run reports as roofline.mfma_busy / roofline.sclk_ghz.
 """
 
 from __future__ import annotations
@@ -38,6 +42,9 @@ METRIC = "attend TFLOP/s + qk_prep GB/s at 1024² Klein shape; % of MI355X roofl
 INFINITY_CACHE_BYTES = 256 * 2 ** 20
 ROOT = os.path.dirname(os.path.abspath(__file__))
 COPY_BYTES = 64 * 2 ** 20       # calibration copy: 64 MiB read + 64 MiB written per launch
+# One rocprofv3 --pmc pass (7 SQ counters + 1 GRBM counter, within one pass's limits).
+MFMA_COUNTERS = ("SQ_VALU_MFMA_BUSY_CYCLES", "SQ_BUSY_CYCLES", "SQ_INSTS_MFMA", "SQ_INSTS_VALU_MFMA_MOPS_BF16",
+                 "SQ_INSTS_VALU_MFMA_MOPS_I8", "SQ_VALU_MFMA_COEXEC_CYCLES", "SQ_INSTS_VALU", "GRBM_GUI_ACTIVE")
 
 
 def parse():
@@ -55,6 +62,8 @@ def parse():
                     help="calibrate: the step plus a plain device copy of known size, for counter runs")
     ap.add_argument("--ingest-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="rocprofv3 --pmc output dirs of FETCH_SIZE / WRITE_SIZE runs of --only calibrate")
+    ap.add_argument("--ingest-mfma", metavar="DIR",
+                    help="rocprofv3 --pmc output dir of a default run with the MFMA_COUNTERS")
     return ap.parse_args()
 
 
@@ -80,6 +89,52 @@ def _counter_means(directory: str, counter: str) -> dict:
         big = max(sums["copy"])
         sums["copy"] = [v for v in sums["copy"] if v >= 0.5 * big]
     return {k: sum(v) / len(v) for k, v in sums.items()}
+
+
+def mfma_file(workload: str) -> str:
+    return os.path.join(ROOT, "profiles", f"mfma_util_{workload}.json")
+
+
+def ingest_mfma(directory: str, workload: str, last: int = 20) -> dict:
+    """MFMA busy fraction and shader clock of attend and the plain int8 GEMM, from one counter
+    run.  Every SQ counter is summed over the GPU: SQ_VALU_MFMA_BUSY_CYCLES over the SIMDs
+    (32 per 32x32 MFMA), SQ_BUSY_CYCLES over the shader engines, so per-SIMD busy cycles /
+    per-engine busy cycles = the matrix pipe's busy fraction, and per-engine busy cycles /
+    the dispatch's duration = the clock.  Means over the last `last` dispatches (warm clock)."""
+    files = glob.glob(os.path.join(directory, "**", "*counter_collection.csv"), recursive=True)
+    agents = glob.glob(os.path.join(directory, "**", "*agent_info.csv"), recursive=True)
+    if not files or not agents:
+        raise SystemExit(f"no counter_collection.csv / agent_info.csv under {directory}")
+    gpu = next(a for a in csv.DictReader(open(agents[0])) if a.get("Simd_Count", "0") not in ("0", ""))
+    simds = int(gpu["Simd_Count"])
+    engines = int(gpu["Cu_Count"]) // int(gpu["Cu_Per_Engine"])
+    rows: dict = {}
+    for f in files:
+        for row in csv.DictReader(open(f)):
+            name = row["Kernel_Name"]
+            key = ("attend" if "attend_kernel" in name else
+                   "w8a8_gemm" if "w8a8_gemm_kernel<false, false" in name else None)
+            if key:
+                d = rows.setdefault(key, {}).setdefault(int(row["Dispatch_Id"]), {})
+                d[row["Counter_Name"]] = float(row["Counter_Value"])
+                d["ns"] = int(row["End_Timestamp"]) - int(row["Start_Timestamp"])
+    out = {"workload": workload, "simds": simds, "shader_engines": engines, "dispatches_averaged": last,
+           "kernels": {}}
+    for key, disp in rows.items():
+        sel = [disp[i] for i in sorted(disp)[-last:]]
+        mean = {c: sum(d.get(c, 0.0) for d in sel) / len(sel) for c in MFMA_COUNTERS + ("ns",)}
+        busy_simd = mean["SQ_VALU_MFMA_BUSY_CYCLES"] / simds
+        cycles = mean["SQ_BUSY_CYCLES"] / engines
+        out["kernels"][key] = {
+            "duration_us": mean["ns"] / 1e3, "mfma_busy_cycles_per_simd": busy_simd,
+            "busy_cycles_per_engine": cycles, "mfma_busy": busy_simd / cycles,
+            "sclk_ghz": cycles / mean["ns"], "mfma_insts": mean["SQ_INSTS_MFMA"],
+            "coexec_cycles_per_simd": mean["SQ_VALU_MFMA_COEXEC_CYCLES"] / simds,
+            "valu_insts": mean["SQ_INSTS_VALU"],
+            "bf16_gflop_counted": mean["SQ_INSTS_VALU_MFMA_MOPS_BF16"] * 512 / 1e9,
+            "i8_gop_counted": mean["SQ_INSTS_VALU_MFMA_MOPS_I8"] * 512 / 1e9,
+            "counters": mean}
+    return out
 
 
 def ingest_pmc(fetch_dir: str, write_dir: str, workload: str) -> dict:
@@ -191,6 +246,13 @@ def w8a8_leg(args, timed, dev) -> dict:
 
 def main() -> int:
     args = parse()
+    if args.ingest_mfma:
+        summary = ingest_mfma(args.ingest_mfma, args.workload)
+        with open(mfma_file(args.workload), "w") as f:
+            json.dump(summary, f, indent=1)
+        print(json.dumps({k: {m: round(v[m], 4) for m in ("mfma_busy", "sclk_ghz", "duration_us")}
+                          for k, v in summary["kernels"].items()}))
+        return 0
     if args.ingest_pmc:
         summary = ingest_pmc(args.ingest_pmc[0], args.ingest_pmc[1], args.workload)
         os.makedirs(os.path.dirname(traffic_file(args.workload)), exist_ok=True)
@@ -280,6 +342,17 @@ def main() -> int:
         with open(traffic_file(w.name)) as f:
             traffic = json.load(f)["kernels"]
     source = os.path.relpath(traffic_file(w.name), ROOT) if traffic else None
+    mfma = {}
+    if os.path.exists(mfma_file(w.name)):
+        with open(mfma_file(w.name)) as f:
+            mfma = json.load(f)["kernels"]
+    mfma_source = os.path.relpath(mfma_file(w.name), ROOT) if mfma else None
+
+    def mfma_fields(kernel: str) -> dict:
+        if kernel not in mfma:
+            return {}
+        return {"mfma_busy": round(mfma[kernel]["mfma_busy"], 4), "sclk_ghz": round(mfma[kernel]["sclk_ghz"], 3),
+                "mfma_source": mfma_source}
 
     result = {
         "metric": METRIC,
@@ -302,7 +375,8 @@ def main() -> int:
                      "unit": "TFLOP/s", "frac": round(at_tflops / BF16_DENSE_PEAK_TFLOPS, 4),
                      "traffic": round(traffic["attend"]["traffic_bytes"]) if traffic else None,
                      "traffic_source": source, "kernel": "attend_kernel",
-                     "flops_per_launch": w.attend_flops(), "avg_launch_us": round(at_ms * 1e3, 2)},
+                     "flops_per_launch": w.attend_flops(), "avg_launch_us": round(at_ms * 1e3, 2),
+                     **mfma_fields("attend")},
         "qk_prep": {"roofline": {"bound": "hbm", "achieved": round(qk_gbs, 1), "peak": HBM_PEAK_GBS,
                                  "unit": "GB/s", "frac": round(qk_gbs / HBM_PEAK_GBS, 4),
                                  "traffic": round(traffic["qk_prep"]["traffic_bytes"]) if traffic else None,
@@ -316,6 +390,7 @@ def main() -> int:
             "achieved": round(ids_gbs, 1), "unit": "GB/s", "frac": round(ids_gbs / HBM_PEAK_GBS, 4)}
     if not args.no_w8a8 and args.only == "step":
         result["w8a8"] = w8a8_leg(args, timed, dev)
+        result["w8a8"]["roofline"].update(mfma_fields("w8a8_gemm"))
     if not args.no_cpu_baseline and args.only == "step":
         result["cpu_baseline"] = cpu_baseline(w, qkv_cpu, qs_cpu, ks_cpu, ids, args.cpu_reps)
     print(json.dumps(result), flush=True)
