@@ -1,0 +1,124 @@
+"""The C ABI on torch's current stream: side streams and captured HIP graphs.
+
+Every entry point launches on the stream it is given (the Python wrappers pass torch's
+current stream) and allocates nothing, so the path runs unchanged on a side stream and
+inside a captured graph.  Graph tests replay several times with new inputs, with eager
+work and synchronisations between the replays, and check every replay against the eager
+result of the same input.
+"""
+
+import math
+
+import pytest
+import torch
+
+from flicker_amd import kernels, rope, w8a8, workloads
+
+pytestmark = pytest.mark.gpu
+D = 128
+
+
+def _case(seed, length=700, heads=8):
+    g = torch.Generator().manual_seed(seed)
+    qkv = torch.randn(1, length, 3 * heads * D, generator=g).to(torch.bfloat16)
+    qs = (1 + 0.05 * torch.randn(D, generator=g)).to(torch.bfloat16)
+    ks = (1 + 0.05 * torch.randn(D, generator=g)).to(torch.bfloat16)
+    ids = rope.sequence_ids(188, 16, 32)   # 188 text + 512 image tokens = 700
+    return qkv, qs, ks, ids, heads
+
+
+def _attention(qkv, qs, ks, freqs, heads):
+    q, k, v = kernels.qk_prep(qkv, qs, ks, freqs, heads, rows=qkv.shape[1])
+    return kernels.attend(q, k, v, block=qkv.shape[1])
+
+
+def test_side_stream_matches_default_stream(device):
+    qkv, qs, ks, ids, heads = _case(1)
+    qkv, qs, ks = qkv.to(device), qs.to(device), ks.to(device)
+    freqs = rope.rope_lanes(ids, 1 / math.sqrt(D), device=device)
+    want = _attention(qkv, qs, ks, freqs, heads)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()   # default priority
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        got = _attention(qkv, qs, ks, freqs, heads)
+    side.synchronize()
+    assert torch.equal(got, want)
+
+    # the int8 projection too
+    x, w = workloads.make_projection(workloads.Projection("t", 300, 384, 768))
+    xd, wd = x.to(device), w.to(device)
+    qw = w8a8.quantize_linear(wd, w8a8.absmax_cols(xd))
+    y_want = w8a8.linear(xd, qw)
+    torch.cuda.synchronize()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        y_got = w8a8.linear(xd, qw)
+    side.synchronize()
+    assert torch.equal(y_got, y_want)
+
+
+def test_graph_replay_qk_prep_attend(device):
+    qkv0, qs, ks, ids, heads = _case(2)
+    qs, ks = qs.to(device), ks.to(device)
+    freqs = rope.rope_lanes(ids, 1 / math.sqrt(D), device=device)
+    length = qkv0.shape[1]
+    static_in = qkv0.to(device)
+    outs = tuple(torch.empty((1, heads, length, D), dtype=torch.bfloat16, device=device) for _ in range(3))
+    static_o = torch.empty_like(outs[0])
+
+    def section():
+        kernels.qk_prep(static_in, qs, ks, freqs, heads, rows=length, out=outs)
+        kernels.attend(*outs, block=length, out=static_o)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        section()                      # warm-up outside the capture
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        section()
+
+    for seed in (3, 4, 5):
+        fresh = _case(seed)[0].to(device)
+        static_in.copy_(fresh)
+        graph.replay()
+        torch.cuda.synchronize()
+        replayed = static_o.clone()
+        eager = _attention(fresh, qs, ks, freqs, heads)   # eager work between replays
+        torch.cuda.synchronize()
+        assert torch.equal(replayed, eager), f"replay with input seed {seed} differs from eager"
+
+
+def test_graph_replay_int8_projection(device):
+    proj = workloads.Projection("t", 512, 384, 3 * 2 * D)
+    x0, w = workloads.make_projection(proj)
+    wd = w.to(device)
+    static_x = x0.to(device)
+    qw = w8a8.quantize_linear(wd, w8a8.absmax_cols(static_x))
+    static_y = torch.empty((proj.tokens, proj.out_features), dtype=torch.bfloat16, device=device)
+
+    def section():
+        xq, a = w8a8.quantize_act(static_x, qw.inv_smooth)
+        w8a8.gemm(xq, a, qw.wq_t, qw.w_scale, out=static_y)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        section()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        section()
+
+    for seed in (7, 8, 9):
+        g = torch.Generator().manual_seed(seed)
+        fresh = torch.randn(proj.tokens, proj.hidden, generator=g).to(torch.bfloat16).to(device)
+        static_x.copy_(fresh)
+        graph.replay()
+        torch.cuda.synchronize()
+        replayed = static_y.clone()
+        eager = w8a8.linear(fresh, qw)
+        torch.cuda.synchronize()
+        assert torch.equal(replayed, eager), f"replay with input seed {seed} differs from eager"
