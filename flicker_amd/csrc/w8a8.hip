@@ -552,13 +552,31 @@ __global__ __launch_bounds__(kGThreads, 2) void w8a8_gemm_kernel(
     float sc[8];
     if (sec < 2) flk::load_scale8<kScaleF32>(sec == 0 ? qe.q_scale : qe.k_scale, l16, sc);
     uint16_t* const out = qe.out[sec];
+    // Row m = b * length + t.  One division for the lane's first row; each read-back moves 4
+    // rows on, which wraps into the next batch entry at most once when length >= 4 (shorter
+    // sequences divide per row).  A division per row measured 2.4% of the fused kernel.
+    const int len = qe.length;
+    const bool short_seq = len < 4;
+    const int m_first = m0 + wm * kGWaveM + (lane >> 4);
+    int b = m_first / len, t = m_first - b * len;
 #pragma unroll 4
     for (int it = 0; it < kReads; ++it) {
       const int ml = it * 4 + (lane >> 4);
-      const uint4 v = *reinterpret_cast<const uint4*>(out_lds + ml * 256 + ((l16 ^ (ml & 15)) * 16));
       const int m = m0 + wm * kGWaveM + ml;
+      if (it > 0) {
+        if (short_seq) {
+          b = m / len;
+          t = m - b * len;
+        } else {
+          t += 4;
+          if (t >= len) {
+            t -= len;
+            ++b;
+          }
+        }
+      }
+      const uint4 v = *reinterpret_cast<const uint4*>(out_lds + ml * 256 + ((l16 ^ (ml & 15)) * 16));
       if (m >= M) continue;   // uniform over the 16-lane row, so the DPP rows stay whole
-      const int b = m / qe.length, t = m - b * qe.length;
       uint4 r = v;
       if (sec < 2) {
         float c[8], s[8];

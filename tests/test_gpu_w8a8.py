@@ -247,6 +247,8 @@ def _fused_case(device, batch, length, heads, k, scale_dtype, gain, seed):
     (1, 4608, 24, 3072, torch.bfloat16, 128 ** -0.5),   # the 1024^2 Klein projection feeding qk_prep
     (2, 257, 2, 256, torch.float32, 1.0),               # ragged token tiles, f32 scales, no gain
     (1, 40, 3, 128, torch.bfloat16, 0.3),
+    (7, 3, 2, 128, torch.bfloat16, 0.5),                # sequences shorter than a read-back step
+    (5, 67, 2, 128, torch.bfloat16, 128 ** -0.5),       # batch entries wrapping inside every tile
 ])
 def test_fused_projection_qk_prep_bit_exact(device, batch, length, heads, k, scale_dtype, gain):
     """flk_w8a8_qk_prep == flk_qk_prep(flk_w8a8_gemm(...)) bit for bit: the epilogue applies
