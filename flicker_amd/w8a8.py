@@ -216,10 +216,15 @@ def qk_prep(x: torch.Tensor, qw: QuantizedLinear, q_scale: torch.Tensor, k_scale
     modulate(x, shift, scale) (modules.py:38-40), computed inside the activation quantisation:
     the whole ``qkv_prep(linear(modulate(x, mod1), w), ...)`` of a block (modules.py:128-133,
     186-190) is then two launches."""
-    from .kernels import HEAD_DIM, Freqs
+    from .kernels import HEAD_DIM, Freqs, PositionIds
 
     if x.dim() != 3:
         raise ValueError(f"x must be (B, L, K), got {tuple(x.shape)}")
+    if isinstance(freqs, PositionIds):
+        # The fused epilogue reads lane tables; build them from the ids with the same
+        # arithmetic the in-kernel form uses, so the values are identical.
+        from .rope import rope_lanes
+        freqs = rope_lanes(freqs.ids, freqs.q_gain, freqs.axes_dim, freqs.theta)
     batch, length, k = x.shape
     if qw.out_features != 3 * num_heads * HEAD_DIM:
         raise ValueError(f"projection has {qw.out_features} outputs, not 3 * {num_heads} * {HEAD_DIM}")

@@ -264,6 +264,17 @@ def test_fused_projection_qk_prep_bit_exact(device, batch, length, heads, k, sca
         assert bad == 0, f"{name}: {bad} of {a.numel()} elements differ"
 
 
+def test_fused_projection_accepts_position_ids(device):
+    """w8a8.qk_prep with PositionIds equals the table form (the lanes are built from the ids)."""
+    from flicker_amd import rope
+    x, qw, qs, ks, freqs, kernels = _fused_case(device, 1, 96, 2, 256, torch.bfloat16, 0.25, seed=3)
+    ids = torch.from_numpy(rope.sequence_ids(32, 8, 8)).to(device)
+    tables = w8a8.qk_prep(x, qw, qs, ks, rope.rope_lanes(ids, 0.25), 2)
+    from_ids = w8a8.qk_prep(x, qw, qs, ks, rope.position_ids(ids, 0.25), 2)
+    torch.cuda.synchronize()
+    assert all(torch.equal(a, b) for a, b in zip(tables, from_ids))
+
+
 def test_fused_projection_writes_at_sequence_offset(device):
     """out/out_offset place the stream inside a joint text|image buffer, as for qk_prep."""
     x, qw, qs, ks, freqs, kernels = _fused_case(device, 1, 64, 2, 128, torch.bfloat16, 0.5, seed=3)
