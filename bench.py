@@ -231,6 +231,18 @@ def w8a8_leg(args, timed, dev) -> dict:
     shift = (0.3 * torch.randn(1, p.hidden, generator=g)).to(torch.bfloat16).to(dev)
     scale = (0.1 * torch.randn(1, p.hidden, generator=g)).to(torch.bfloat16).to(dev)
     mod_ms = timed(lambda i: w8a8.quantize_act_modulated(x3, shift, scale, qw.inv_smooth), args.steps)
+    # A block's whole attention section on this path (modules.py:128-133 + 157 for one stream):
+    # modulate + int8 quantisation, the projection with qk_prep in its epilogue, attention
+    # with merge_heads in its epilogue -- three launches.
+    merged = [torch.empty((1, p.tokens, heads * 128), dtype=torch.bfloat16, device=dev) for _ in range(2)]
+
+    def section(i):
+        o = qkv_out[i % 2]
+        w8a8.qk_prep(x3, qw, qs, ks, freqs, heads, out=o, modulation=(shift, scale))
+        kernels.attend_merged(*o, out=merged[i % 2])
+
+    section(0)
+    section_ms = timed(section, args.steps)
     del x3
     return {"workload": f"{p.name}: X ({p.tokens}, {p.hidden}) bf16 with {p.outlier_fraction:.0%} outlier "
                         f"channels x{p.outlier_gain:g}, W ({p.hidden}, {p.out_features}) ~ N(0, 0.02)",
@@ -241,6 +253,8 @@ def w8a8_leg(args, timed, dev) -> dict:
             "modulate_quantize_act_us": round(mod_ms * 1e3, 2),
             "gemm_then_qk_prep_us": round(unfused_ms * 1e3, 2),
             "fused_gemm_qk_prep_us": round(fused_ms * 1e3, 2),
+            "block_section_us": round(section_ms * 1e3, 2),
+            "block_section": "modulate+quantise -> int8 projection with qk_prep epilogue -> attend_merged",
             "dtype": "int8 operands, int32 accumulate, bf16 out"}
 
 
