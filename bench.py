@@ -82,6 +82,7 @@ def _counter_means(directory: str, counter: str) -> dict:
                 continue
             name = row["Kernel_Name"]
             key = ("attend" if "attend_kernel" in name else "qk_prep" if "qk_prep_kernel" in name
+                   else "w8a8_gemm" if "w8a8_gemm_kernel<false, false" in name
                    else "copy" if ("copyBuffer" in name or "copy" in name.lower()) else None)
             if key:
                 sums.setdefault(key, []).append(float(row["Counter_Value"]))
@@ -146,7 +147,9 @@ def ingest_pmc(fetch_dir: str, write_dir: str, workload: str) -> dict:
     w_scale = COPY_BYTES / (write["copy"] * 1024)
     out = {"workload": workload, "fetch_scale": f_scale, "write_scale": w_scale,
            "copy_fetch_kib": fetch["copy"], "copy_write_kib": write["copy"], "kernels": {}}
-    for k in ("qk_prep", "attend"):
+    for k in ("qk_prep", "attend", "w8a8_gemm"):
+        if k not in fetch or k not in write:
+            continue
         rb, wb = fetch[k] * 1024 * f_scale, write[k] * 1024 * w_scale
         out["kernels"][k] = {"fetch_kib": fetch[k], "write_kib": write[k], "read_bytes": rb,
                              "write_bytes": wb, "traffic_bytes": rb + wb}
@@ -176,6 +179,17 @@ def cpu_baseline(w, qkv, qs, ks, ids, reps: int) -> dict:
                       f"p50 of {reps} after 1 warm-up"}
 
 
+def projection_operands(p, dev):
+    """The projection's calibrated int8 operands: (x, qw, xq, a_scale)."""
+    from flicker_amd import w8a8, workloads
+
+    x_cpu, w_cpu = workloads.make_projection(p)
+    x, wt = x_cpu.to(dev), w_cpu.to(dev)
+    qw = w8a8.quantize_linear(wt, w8a8.absmax_cols(x))
+    xq, a_scale = w8a8.quantize_act(x, qw.inv_smooth)
+    return x, qw, xq, a_scale
+
+
 def w8a8_leg(args, timed, dev) -> dict:
     """The int8 SmoothQuant QKV projection feeding qk_prep (X (M, 3072) -> Y (M, 9216)):
     activation quantisation and the int8-MFMA GEMM, each timed back to back."""
@@ -184,10 +198,7 @@ def w8a8_leg(args, timed, dev) -> dict:
     from flicker_amd import w8a8, workloads
 
     p = workloads.PROJECTIONS[args.projection]
-    x_cpu, w_cpu = workloads.make_projection(p)
-    x, wt = x_cpu.to(dev), w_cpu.to(dev)
-    qw = w8a8.quantize_linear(wt, w8a8.absmax_cols(x))
-    xq, a_scale = w8a8.quantize_act(x, qw.inv_smooth)
+    x, qw, xq, a_scale = projection_operands(p, dev)
     ys = [torch.empty((p.tokens, p.out_features), dtype=torch.bfloat16, device=dev) for _ in range(2)]
     for i in range(20):
         w8a8.gemm(xq, a_scale, qw.wq_t, qw.w_scale, out=ys[i % 2])
@@ -304,10 +315,17 @@ def main() -> int:
         o = torch.empty_like(out[0])
         sets.append((qkv, out, o))
     copies = []
+    calib_gemm = None
     if args.only == "calibrate":
         for _ in range(4):
             copies.append((torch.empty(COPY_BYTES, dtype=torch.uint8, device=dev).fill_(1),
                            torch.empty(COPY_BYTES, dtype=torch.uint8, device=dev)))
+        if not args.no_w8a8:   # the plain int8 GEMM too, for its traffic
+            from flicker_amd import w8a8
+            proj = workloads.PROJECTIONS[args.projection]
+            _, cqw, cxq, ca = projection_operands(proj, dev)
+            cy = torch.empty((proj.tokens, proj.out_features), dtype=torch.bfloat16, device=dev)
+            calib_gemm = lambda: w8a8.gemm(cxq, ca, cqw.wq_t, cqw.w_scale, out=cy)  # noqa: E731
 
     def run_qk(i):
         qkv, out, _ = sets[i % n_sets]
@@ -327,6 +345,8 @@ def main() -> int:
         if copies:
             src, dst = copies[i % len(copies)]
             dst.copy_(src)
+        if calib_gemm is not None:
+            calib_gemm()
 
     def timed(fn, n):
         """Average ms per call of n back-to-back calls between one pair of HIP events on the
@@ -404,7 +424,12 @@ def main() -> int:
             "achieved": round(ids_gbs, 1), "unit": "GB/s", "frac": round(ids_gbs / HBM_PEAK_GBS, 4)}
     if not args.no_w8a8 and args.only == "step":
         result["w8a8"] = w8a8_leg(args, timed, dev)
+        proj = workloads.PROJECTIONS[args.projection]
         result["w8a8"]["roofline"].update(mfma_fields("w8a8_gemm"))
+        result["w8a8"]["roofline"]["bytes_per_launch"] = proj.gemm_bytes()
+        if "w8a8_gemm" in traffic and proj.tokens == w.batch * w.length:
+            result["w8a8"]["roofline"]["traffic"] = round(traffic["w8a8_gemm"]["traffic_bytes"])
+            result["w8a8"]["roofline"]["traffic_source"] = source
     if not args.no_cpu_baseline and args.only == "step":
         result["cpu_baseline"] = cpu_baseline(w, qkv_cpu, qs_cpu, ks_cpu, ids, args.cpu_reps)
     print(json.dumps(result), flush=True)

@@ -85,6 +85,11 @@ class Projection:
     outlier_fraction: float = 0.01
     outlier_gain: float = 20.0
 
+    def gemm_bytes(self) -> int:
+        """Algorithmic HBM bytes of one int8 GEMM: Xq (M, K) and WqT (N, K) int8 read once,
+        Y (M, N) bf16 written (scales negligible)."""
+        return self.tokens * self.hidden + self.hidden * self.out_features + 2 * self.tokens * self.out_features
+
     def gemm_ops(self) -> int:
         """2 M K N integer multiply-adds counted as two ops each."""
         return 2 * self.tokens * self.hidden * self.out_features
