@@ -371,6 +371,23 @@ def main() -> int:
     qk_ids_ms = timed(run_qk_ids, args.steps) if args.only == "step" else None
     at_tflops = w.attend_flops() / (at_ms * 1e-3) / 1e12
 
+    def p50_launch_us(fn, reps: int = 30) -> float:
+        """The reference's method (tools/bench.py:21,25-33): the median of single calls, each
+        between its own pair of events (reads high for short kernels: the events' own cost)."""
+        durs = []
+        for i in range(reps):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            fn(i)
+            e1.record()
+            e1.synchronize()
+            durs.append(e0.elapsed_time(e1) * 1e3)
+        durs.sort()
+        return round(durs[len(durs) // 2], 2)
+
+    at_p50 = p50_launch_us(run_attend) if args.only == "step" else None
+    qk_p50 = p50_launch_us(run_qk) if args.only == "step" else None
+
     traffic = {}
     if os.path.exists(traffic_file(w.name)):
         with open(traffic_file(w.name)) as f:
@@ -410,12 +427,14 @@ def main() -> int:
                      "traffic": round(traffic["attend"]["traffic_bytes"]) if traffic else None,
                      "traffic_source": source, "kernel": "attend_kernel",
                      "flops_per_launch": w.attend_flops(), "avg_launch_us": round(at_ms * 1e3, 2),
+                     "p50_launch_us": at_p50,
                      **mfma_fields("attend")},
         "qk_prep": {"roofline": {"bound": "hbm", "achieved": round(qk_gbs, 1), "peak": HBM_PEAK_GBS,
                                  "unit": "GB/s", "frac": round(qk_gbs / HBM_PEAK_GBS, 4),
                                  "traffic": round(traffic["qk_prep"]["traffic_bytes"]) if traffic else None,
                                  "traffic_source": source, "kernel": "qk_prep_kernel",
-                                 "bytes_per_launch": w.qk_prep_bytes(), "avg_launch_us": round(qk_ms * 1e3, 2)}},
+                                 "bytes_per_launch": w.qk_prep_bytes(), "avg_launch_us": round(qk_ms * 1e3, 2),
+                                 "p50_launch_us": qk_p50}},
     }
     if qk_ids_ms is not None:
         ids_gbs = w.qk_prep_bytes(tables=False) / (qk_ids_ms * 1e-3) / 1e9
