@@ -33,8 +33,12 @@ namespace {
 
 constexpr int kHeadDim = 128;
 constexpr int kLanesPerRow = 16;
-constexpr int kThreads = 256;
+#ifndef FLK_QK_THREADS
+#define FLK_QK_THREADS 256
+#endif
+constexpr int kThreads = FLK_QK_THREADS;   // block size (a tuning knob): 16 lanes per token row
 constexpr int kTokensPerBlock = kThreads / kLanesPerRow;
+static_assert(kThreads % 64 == 0 && kThreads <= 1024, "whole waves, at most 1024 threads");
 
 // Cache policy of the streaming accesses (bit 0: QKV loads, bit 1: Q/K/V stores) and a
 // forced heads-per-group (0 = automatic); compile-time knobs for tuning sweeps.  The QKV
