@@ -89,6 +89,24 @@ def stream_of(t: torch.Tensor) -> int:
     return torch.cuda.current_stream(t.device).cuda_stream
 
 
+def device_of(*tensors) -> torch.device:
+    """The one GPU that every given tensor (None entries skipped) lives on."""
+    devices = {t.device for t in tensors if t is not None}
+    if len(devices) != 1:
+        raise ValueError(f"the operands of one call must share one GPU, got {sorted(map(str, devices))}")
+    device = devices.pop()
+    if device.type != "cuda":
+        raise ValueError(f"operands are on {device}; flicker_amd runs its kernels on the GPU only")
+    return device
+
+
+def run(name: str, tensors, *args) -> None:
+    """Call entry point ``name`` with the tensors' GPU current -- a HIP launch goes to the
+    current device, whatever device the tensors live on -- and raise on a non-zero status."""
+    with torch.cuda.device(device_of(*tensors)):
+        check(getattr(lib(), name)(*args), name)
+
+
 def ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
 

@@ -88,8 +88,8 @@ def lane_pair(freqs: torch.Tensor, q_gain: float = 1.0) -> Freqs:
     length, pairs = pe.shape[0], pe.shape[1]
     cos = torch.empty((length, 2 * pairs), dtype=torch.float32, device=pe.device)
     sin = torch.empty_like(cos)
-    _lib.check(_lib.lib().flk_lane_pair(pe.data_ptr(), length, pairs, cos.data_ptr(), sin.data_ptr(),
-                                        _lib.stream_of(pe)), "flk_lane_pair")
+    _lib.run("flk_lane_pair", (pe, cos, sin), pe.data_ptr(), length, pairs, cos.data_ptr(), sin.data_ptr(),
+             _lib.stream_of(pe))
     return Freqs(cos, sin, float(q_gain))
 
 
@@ -172,16 +172,14 @@ def _launch_qk_prep(qkv, q_scale, k_scale, freqs, num_heads: int, out, out_offse
               batch, length, num_heads, head_dim, out[0].data_ptr(), out[1].data_ptr(), out[2].data_ptr(),
               out_length, out_offset, _lib.stream_of(qkv))
     if isinstance(freqs, PositionIds):
-        status = _lib.lib().flk_qk_prep_ids(
-            qkv.data_ptr(), qkv.stride(0), qkv.stride(1), rope.data_ptr(), rope.stride(0),
-            len(freqs.axes_dim), _lib.int_array(freqs.axes_dim), float(freqs.theta), *common)
-        _lib.check(status, "flk_qk_prep_ids")
+        _lib.run("flk_qk_prep_ids", (qkv, rope, q_scale, k_scale, *out),
+                 qkv.data_ptr(), qkv.stride(0), qkv.stride(1), rope.data_ptr(), rope.stride(0),
+                 len(freqs.axes_dim), _lib.int_array(freqs.axes_dim), float(freqs.theta), *common)
     else:
         cos, sin = rope
-        status = _lib.lib().flk_qk_prep(
-            qkv.data_ptr(), qkv.stride(0), qkv.stride(1), cos.data_ptr(), sin.data_ptr(), cos.stride(0),
-            *common)
-        _lib.check(status, "flk_qk_prep")
+        _lib.run("flk_qk_prep", (qkv, cos, sin, q_scale, k_scale, *out),
+                 qkv.data_ptr(), qkv.stride(0), qkv.stride(1), cos.data_ptr(), sin.data_ptr(), cos.stride(0),
+                 *common)
     return out
 
 
@@ -276,15 +274,12 @@ def attend_merged(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
         raise ValueError(f"out must be a bf16 ({batch}, {length}, {heads * dim}) view with contiguous, "
                          "4-element aligned rows")
     _on_gpu("out", out)
-    status = _lib.lib().flk_attend_to(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
-                                      batch, heads, length, dim, out.stride(0), dim, out.stride(1),
-                                      _lib.stream_of(q))
-    _lib.check(status, "flk_attend_to")
+    _lib.run("flk_attend_to", (q, k, v, out), q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+             batch, heads, length, dim, out.stride(0), dim, out.stride(1), _lib.stream_of(q))
     return out
 
 
 def _launch_attend(q, k, v, out) -> None:
     batch, heads, length, dim = q.shape
-    status = _lib.lib().flk_attend(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
-                                   batch, heads, length, dim, _lib.stream_of(q))
-    _lib.check(status, "flk_attend")
+    _lib.run("flk_attend", (q, k, v, out), q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+             batch, heads, length, dim, _lib.stream_of(q))

@@ -58,9 +58,8 @@ def embed_nd(ids, axes_dim=_KLEIN.axes_dim, theta: float = _KLEIN.theta, device=
     pairs = sum(axes_dim) // 2
     pe = torch.empty((batch, 1, length, pairs, 2, 2), dtype=torch.float32, device=ids.device)
     flat = ids.reshape(batch * length, n_axes)
-    _lib.check(_lib.lib().flk_rope_embed(flat.data_ptr(), n_axes, batch * length, n_axes,
-                                         _lib.int_array(axes_dim), float(theta), pe.data_ptr(),
-                                         _lib.stream_of(pe)), "flk_rope_embed")
+    _lib.run("flk_rope_embed", (flat, pe), flat.data_ptr(), n_axes, batch * length, n_axes,
+             _lib.int_array(axes_dim), float(theta), pe.data_ptr(), _lib.stream_of(pe))
     return pe
 
 
@@ -85,9 +84,8 @@ def rope_lanes(ids, q_gain: float = 1.0, axes_dim=_KLEIN.axes_dim, theta: float 
     width = sum(axes_dim)
     cos = torch.empty((length, width), dtype=torch.float32, device=ids.device)
     sin = torch.empty_like(cos)
-    _lib.check(_lib.lib().flk_rope_lanes(ids.data_ptr(), n_axes, length, n_axes, _lib.int_array(axes_dim),
-                                         float(theta), cos.data_ptr(), sin.data_ptr(), _lib.stream_of(cos)),
-               "flk_rope_lanes")
+    _lib.run("flk_rope_lanes", (ids, cos, sin), ids.data_ptr(), n_axes, length, n_axes,
+             _lib.int_array(axes_dim), float(theta), cos.data_ptr(), sin.data_ptr(), _lib.stream_of(cos))
     return Freqs(cos, sin, float(q_gain))
 
 

@@ -70,8 +70,8 @@ def absmax_rows(w: torch.Tensor) -> torch.Tensor:
     """Per-row max |w| of a bf16 (K, N) weight: the max_o |W[j,o]| of the smoothing factor."""
     w = _rows("w", w)
     out = torch.empty(w.shape[0], dtype=torch.float32, device=w.device)
-    _lib.check(_lib.lib().flk_absmax_rows(w.data_ptr(), w.shape[0], w.shape[1], w.stride(0), out.data_ptr(),
-                                          _lib.stream_of(w)), "flk_absmax_rows")
+    _lib.run("flk_absmax_rows", (w, out), w.data_ptr(), w.shape[0], w.shape[1], w.stride(0), out.data_ptr(),
+             _lib.stream_of(w))
     return out
 
 
@@ -85,8 +85,8 @@ def absmax_cols(x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tenso
         out = torch.empty(k, dtype=torch.float32, device=x.device)
     elif out.shape != (k,) or out.dtype != torch.float32 or not out.is_contiguous() or out.device != x.device:
         raise ValueError(f"out must be a contiguous float32 ({k},) tensor on {x.device}")
-    _lib.check(_lib.lib().flk_absmax_cols(x.data_ptr(), x.shape[0], k, x.stride(0), int(accumulate),
-                                          out.data_ptr(), _lib.stream_of(x)), "flk_absmax_cols")
+    _lib.run("flk_absmax_cols", (x, out), x.data_ptr(), x.shape[0], k, x.stride(0), int(accumulate),
+             out.data_ptr(), _lib.stream_of(x))
     return out
 
 
@@ -97,8 +97,8 @@ def smooth_factors(x_absmax: torch.Tensor, w_absmax: torch.Tensor) -> tuple[torc
     wa = _f32("w_absmax", w_absmax, k, xa.device)
     s = torch.empty_like(xa)
     inv = torch.empty_like(xa)
-    _lib.check(_lib.lib().flk_smooth_factors(xa.data_ptr(), wa.data_ptr(), k, s.data_ptr(), inv.data_ptr(),
-                                             _lib.stream_of(xa)), "flk_smooth_factors")
+    _lib.run("flk_smooth_factors", (xa, wa, s, inv), xa.data_ptr(), wa.data_ptr(), k, s.data_ptr(),
+             inv.data_ptr(), _lib.stream_of(xa))
     return s, inv
 
 
@@ -109,8 +109,8 @@ def quantize_weight(w: torch.Tensor, smooth: torch.Tensor) -> tuple[torch.Tensor
     s = _f32("smooth", smooth, k, w.device)
     wq_t = torch.empty((n, k), dtype=torch.int8, device=w.device)
     w_scale = torch.empty(n, dtype=torch.float32, device=w.device)
-    _lib.check(_lib.lib().flk_quantize_weight(w.data_ptr(), w.stride(0), s.data_ptr(), k, n, wq_t.data_ptr(),
-                                              w_scale.data_ptr(), _lib.stream_of(w)), "flk_quantize_weight")
+    _lib.run("flk_quantize_weight", (w, s, wq_t, w_scale), w.data_ptr(), w.stride(0), s.data_ptr(), k, n,
+             wq_t.data_ptr(), w_scale.data_ptr(), _lib.stream_of(w))
     return wq_t, w_scale
 
 
@@ -128,8 +128,8 @@ def quantize_act(x: torch.Tensor, inv_smooth: torch.Tensor) -> tuple[torch.Tenso
     inv = _f32("inv_smooth", inv_smooth, k, x.device)
     xq = torch.empty((m, k), dtype=torch.int8, device=x.device)
     a_scale = torch.empty(m, dtype=torch.float32, device=x.device)
-    _lib.check(_lib.lib().flk_quantize_act(x.data_ptr(), x.stride(0), inv.data_ptr(), m, k, xq.data_ptr(),
-                                           a_scale.data_ptr(), _lib.stream_of(x)), "flk_quantize_act")
+    _lib.run("flk_quantize_act", (x, inv, xq, a_scale), x.data_ptr(), x.stride(0), inv.data_ptr(), m, k,
+             xq.data_ptr(), a_scale.data_ptr(), _lib.stream_of(x))
     return xq, a_scale
 
 
@@ -163,9 +163,9 @@ def quantize_act_modulated(x: torch.Tensor, shift: torch.Tensor, scale: torch.Te
         out = x_mod
         if out.shape != (batch, length, k) or out.dtype != torch.bfloat16 or not out.is_contiguous():
             raise ValueError(f"x_mod must be a contiguous bfloat16 ({batch}, {length}, {k}) tensor")
-    _lib.check(_lib.lib().flk_quantize_act_modulated(
-        xr.data_ptr(), xr.stride(0), shift.data_ptr(), scale.data_ptr(), shift.stride(0), length, inv.data_ptr(),
-        m, k, xq.data_ptr(), a_scale.data_ptr(), _lib.ptr(out), k, _lib.stream_of(x)), "flk_quantize_act_modulated")
+    _lib.run("flk_quantize_act_modulated", (xr, shift, scale, inv, xq, a_scale, out),
+             xr.data_ptr(), xr.stride(0), shift.data_ptr(), scale.data_ptr(), shift.stride(0), length,
+             inv.data_ptr(), m, k, xq.data_ptr(), a_scale.data_ptr(), _lib.ptr(out), k, _lib.stream_of(x))
     return (xq, a_scale) if out is None else (xq, a_scale, out)
 
 
@@ -190,9 +190,8 @@ def gemm(xq: torch.Tensor, a_scale: torch.Tensor, wq_t: torch.Tensor, w_scale: t
         raise ValueError(f"out must be a bfloat16 ({m}, {n}) view with contiguous rows")
     if acc is not None and (acc.shape != (m, n) or acc.dtype != torch.int32 or not acc.is_contiguous()):
         raise ValueError(f"acc must be a contiguous int32 ({m}, {n}) tensor")
-    _lib.check(_lib.lib().flk_w8a8_gemm(xq.data_ptr(), wq_t.data_ptr(), a.data_ptr(), ws.data_ptr(), m, k, n,
-                                        out.data_ptr(), out.stride(0), _lib.ptr(acc), _lib.stream_of(xq)),
-               "flk_w8a8_gemm")
+    _lib.run("flk_w8a8_gemm", (xq, wq_t, a, ws, out, acc), xq.data_ptr(), wq_t.data_ptr(), a.data_ptr(),
+             ws.data_ptr(), m, k, n, out.data_ptr(), out.stride(0), _lib.ptr(acc), _lib.stream_of(xq))
     return out
 
 
@@ -258,10 +257,9 @@ def qk_prep(x: torch.Tensor, qw: QuantizedLinear, q_scale: torch.Tensor, k_scale
                 raise ValueError("out tensors must be contiguous bf16 (B, H, L_out, D) of one shape")
         if out_offset < 0 or out_offset + length > out_length:
             raise ValueError(f"out_offset {out_offset} + L {length} exceeds the output length {out_length}")
-    _lib.check(_lib.lib().flk_w8a8_qk_prep(
-        xq.data_ptr(), qw.wq_t.data_ptr(), a_scale.data_ptr(), qw.w_scale.data_ptr(), k, cos.data_ptr(),
-        sin.data_ptr(), cos.stride(0), q_scale.data_ptr(), k_scale.data_ptr(),
-        int(q_scale.dtype == torch.float32), float(q_gain), batch, length, num_heads, HEAD_DIM,
-        out[0].data_ptr(), out[1].data_ptr(), out[2].data_ptr(), out_length, out_offset,
-        _lib.stream_of(x)), "flk_w8a8_qk_prep")
+    _lib.run("flk_w8a8_qk_prep", (xq, qw.wq_t, a_scale, qw.w_scale, cos, sin, q_scale, k_scale, *out),
+             xq.data_ptr(), qw.wq_t.data_ptr(), a_scale.data_ptr(), qw.w_scale.data_ptr(), k, cos.data_ptr(),
+             sin.data_ptr(), cos.stride(0), q_scale.data_ptr(), k_scale.data_ptr(),
+             int(q_scale.dtype == torch.float32), float(q_gain), batch, length, num_heads, HEAD_DIM,
+             out[0].data_ptr(), out[1].data_ptr(), out[2].data_ptr(), out_length, out_offset, _lib.stream_of(x))
     return out

@@ -211,6 +211,21 @@ def test_cpu_baseline_matches_oracle_plain_path():
     assert np.abs(got - want).max() <= 2e-2 and np.abs(got - want).mean() <= 2e-4
 
 
+def test_operands_must_share_one_gpu():
+    """Every call names its operands; they must live on one GPU, which is made current for
+    the launch (a HIP launch goes to the current device, not to the operands' one)."""
+    import types
+    on0 = types.SimpleNamespace(device=torch.device("cuda", 0))
+    on1 = types.SimpleNamespace(device=torch.device("cuda", 1))
+    assert _lib.device_of(on0, None, on0) == torch.device("cuda", 0)
+    with pytest.raises(ValueError, match="share one GPU"):
+        _lib.device_of(on0, on1)
+    with pytest.raises(ValueError, match="GPU only"):
+        _lib.device_of(torch.zeros(1))
+    with pytest.raises(ValueError, match="share one GPU"):
+        _lib.device_of(on0, torch.zeros(1))
+
+
 def test_bench_refuses_multi_gpu():
     proc = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"],
                           capture_output=True, text=True, timeout=120)
