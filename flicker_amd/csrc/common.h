@@ -41,19 +41,19 @@ __device__ __forceinline__ float row16_sum(float v) {
 // Copy 16 bytes per lane from global memory straight into LDS (global_load_lds_dwordx4):
 // lane i of the wave lands at lds_dst + 16 i, where lds_dst must be wave-uniform.  Issued
 // from inline asm so the compiler does not order later LDS reads behind it (it cannot
-// prove the destination disjoint from them); callers wait with s_waitcnt vmcnt.
+// prove the destination disjoint from them); callers wait with s_waitcnt vmcnt.  The LDS
+// address is an M0 operand ("{m0}"), so the compiler writes M0 itself and knows it is in use;
+// the s_nop is the wait state an M0 write needs before an LDS DMA reads it.
 __device__ __forceinline__ void dma16(const void* src, const uint8_t* lds_dst) {
-  const unsigned m0 = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)lds_dst);
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
-               :: "s"(m0), "v"(src) : "memory", "m0");
+  const unsigned lds = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)lds_dst);
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %1, off" :: "{m0}"(lds), "v"(src) : "memory");
 }
 
 // The same copy from a wave-uniform base (scalar registers) plus a 32-bit per-lane byte
 // offset: one VGPR per source instead of a 64-bit address.
 __device__ __forceinline__ void dma16_at(const void* base, uint32_t voff, const uint8_t* lds_dst) {
-  const unsigned m0 = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)lds_dst);
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
-               :: "s"(m0), "v"(voff), "s"(base) : "memory", "m0");
+  const unsigned lds = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)lds_dst);
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %1, %2" :: "{m0}"(lds), "v"(voff), "s"(base) : "memory");
 }
 
 __device__ __forceinline__ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
