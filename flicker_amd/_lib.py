@@ -26,6 +26,8 @@ SIGNATURES = {
                              _p, _p, _p, _i64, _i64, _p]),
     "flk_attend": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _p]),
     "flk_attend_to": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _i64, _i64, _i64, _p]),
+    "flk_attend_split_to": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _i64, _i64, _i64, _i, _p, _i64, _p]),
+    "flk_attend_plan": (_i, [_i, _i, _i, _ip, ctypes.POINTER(ctypes.c_int64)]),
     "flk_rope_embed": (_i, [_p, _i64, _i64, _i, _ip, _f, _p, _p]),
     "flk_lane_pair": (_i, [_p, _i64, _i, _p, _p, _p]),
     "flk_rope_lanes": (_i, [_p, _i64, _i64, _i, _ip, _f, _p, _p, _p]),
@@ -109,6 +111,14 @@ def run(name: str, tensors, *args) -> None:
 
 def ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
+
+
+def attend_plan(batch: int, heads: int, length: int) -> tuple[int, int]:
+    """(splits, workspace bytes) that flk_attend_plan picks for an attend of this shape."""
+    splits, nbytes = ctypes.c_int(0), ctypes.c_int64(0)
+    check(lib().flk_attend_plan(batch, heads, length, ctypes.byref(splits), ctypes.byref(nbytes)),
+          "flk_attend_plan")
+    return splits.value, nbytes.value
 
 
 def int_array(values) -> ctypes.Array:

@@ -46,6 +46,8 @@
 // so that all query tiles of one head run on the same XCD (hardware deals blocks
 // round-robin over the 8 XCDs), keeping the head's K/V in one L2.
 
+#include <algorithm>
+
 #include "common.h"
 
 namespace {
@@ -75,6 +77,7 @@ constexpr float kLog2e = 1.4426950408889634f;
 using flk::bf16x2;
 using flk::bf16x8;
 using flk::f32x16;
+using flk::f32x4;
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef short s16x8 __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
@@ -223,20 +226,30 @@ __device__ __forceinline__ void iteration(WaveState& w, const Ctx& c, int t, int
   asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" :: "n"(kDmaPerIter) : "memory");
 }
 
+// kSplit = false: the block takes every key of its 256 queries and writes O.
+// kSplit = true: the keys are cut into `splits` ranges of whole 4-tile groups (so ring
+// positions stay literal in the unrolled loop); the block takes one range and writes its
+// unnormalised acc and l to part_acc / part_l, which attend_merge_kernel sums.  Without a
+// running max the partial sums of different key ranges add as they are.
+template <bool kSplit>
 __global__ __launch_bounds__(kThreads, 2) void attend_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, uint16_t* __restrict__ o, int length, int q_blocks,
-    int total_blocks, int heads, int64_t o_batch_stride, int64_t o_head_stride, int64_t o_row_stride) {
+    int total_blocks, int heads, int splits, int64_t o_batch_stride, int64_t o_head_stride,
+    int64_t o_row_stride, float* __restrict__ part_acc, float* __restrict__ part_l) {
   __shared__ __attribute__((aligned(1024))) uint8_t smem[kSmemBytes];
 
   // XCD-aware renumbering: hardware block id p runs on XCD p % 8; give each XCD a
-  // contiguous range of logical ids (head-major), so a head's query tiles share an L2.
+  // contiguous range of logical ids (head-major, then split, then query tile), so the
+  // query tiles that read one head's keys share an L2.
   const int p = blockIdx.x;
   const int xcd = p % kXcds, local = p / kXcds;
   const int per = total_blocks / kXcds, extra = total_blocks % kXcds;
   const int logical = xcd * per + min(xcd, extra) + local;
-  const int bh = logical / q_blocks;
-  const int qblk = logical - bh * q_blocks;
+  const int qblk = logical % q_blocks;
+  const int rest = logical / q_blocks;
+  const int split = kSplit ? rest % splits : 0;
+  const int bh = kSplit ? rest / splits : rest;
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
@@ -247,6 +260,12 @@ __global__ __launch_bounds__(kThreads, 2) void attend_kernel(
   c.length = length;
   c.ntiles = (length + kBN - 1) / kBN;
   c.cp.last_tile = c.ntiles - 1;
+  int t_begin = 0, t_end = c.ntiles;   // this block's key tiles
+  if constexpr (kSplit) {
+    const int groups = (c.ntiles + 3) / 4;
+    t_begin = 4 * (split * groups / splits);
+    t_end = min(4 * ((split + 1) * groups / splits), c.ntiles);
+  }
   c.cp.lds_wave_off = __builtin_amdgcn_readfirstlane(wave * kRowsPerWave * kRowBytes);
   {
     const int rows_last = length - c.cp.last_tile * kBN;   // 1..64 valid rows in the last tile
@@ -264,9 +283,10 @@ __global__ __launch_bounds__(kThreads, 2) void attend_kernel(
   c.kh = k + head_off;
   c.vh = v + head_off;
 
-  // Prologue copies: K tiles 0-2, V tiles 0-1.
-  for (int tl = 0; tl < 3; ++tl) copy_tile(smem + tl * kTileBytes, c.kh, tl, c.cp);
-  for (int tl = 0; tl < 2; ++tl) copy_tile(smem + kVRing + tl * kTileBytes, c.vh, tl, c.cp);
+  // Prologue copies: K tiles t_begin .. +2, V tiles t_begin .. +1 (ring slots 0-2 and 0-1:
+  // t_begin is a multiple of 4).
+  for (int tl = 0; tl < 3; ++tl) copy_tile(smem + tl * kTileBytes, c.kh, t_begin + tl, c.cp);
+  for (int tl = 0; tl < 2; ++tl) copy_tile(smem + kVRing + tl * kTileBytes, c.vh, t_begin + tl, c.cp);
 
   WaveState w;
   const int q0 = qblk * kBM + wave * 32;
@@ -319,21 +339,21 @@ __global__ __launch_bounds__(kThreads, 2) void attend_kernel(
 
   // Unrolled main loop over full tiles, then the remaining (at most 3 full and one partial)
   // tiles with key masking and a computed ring position.
-  const int full_tiles = length / kBN;
-  int t = 0;
-  for (; t + 4 <= full_tiles; t += 4) {
+  const int full_end = min(length / kBN, t_end);
+  int t = t_begin;
+  for (; t + 4 <= full_end; t += 4) {
     iteration<false>(w, c, t, 0);
     iteration<false>(w, c, t + 1, 1);
     iteration<false>(w, c, t + 2, 2);
     iteration<false>(w, c, t + 3, 3);
   }
-  for (; t < c.ntiles; ++t) iteration<true>(w, c, t, t & 3);
+  for (; t < t_end; ++t) iteration<true>(w, c, t, t & 3);
   // No copy may still be writing this block's LDS when the block ends.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   // Drain: O^T += V(U-1)^T P(U-1)^T for the last unit (unit 1 of the last tile).
   {
-    const uint8_t* v_last = smem + kVRing + ((c.ntiles - 1) & 3) * kTileBytes + kUnitBytes;
+    const uint8_t* v_last = smem + kVRing + ((t_end - 1) & 3) * kTileBytes + kUnitBytes;
     const bf16x8 pb0 = __builtin_bit_cast(bf16x8, make_uint4(w.pB[0], w.pB[1], w.pB[2], w.pB[3]));
     const bf16x8 pb1 = __builtin_bit_cast(bf16x8, make_uint4(w.pB[4], w.pB[5], w.pB[6], w.pB[7]));
 #pragma unroll
@@ -344,7 +364,23 @@ __global__ __launch_bounds__(kThreads, 2) void attend_kernel(
 
   // Epilogue: l over both lane halves, O = bf16(acc / l), 4 d values per 8-byte store.
   const float l = w.lsum + __shfl_xor(w.lsum, 32);
-  if (qi < length) {
+  if constexpr (kSplit) {
+    // Partials in the accumulator's own lane order, so each store is 64 lanes x 16 bytes
+    // contiguous: with unit = bh * q_blocks + qblk, register group i = 4m + r holds
+    // acc[d = 32m + 8r + 4g .. +3] of query qi at float4 index
+    //   ((split * units + unit) * 8 + wave) * 1024 + i * 64 + lane,
+    // and l at ((split * units + unit) * 8 + wave) * 64 + lane.
+    const int64_t units = total_blocks / splits;
+    const int64_t slot = ((int64_t)split * units + (int64_t)bh * q_blocks + qblk) * kWaves + wave;
+    f32x4* dst = reinterpret_cast<f32x4*>(part_acc) + slot * 1024 + lane;
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        dst[(m * 4 + r) * 64] = f32x4{w.oacc[m][r * 4 + 0], w.oacc[m][r * 4 + 1], w.oacc[m][r * 4 + 2],
+                                      w.oacc[m][r * 4 + 3]};
+    part_l[slot * 64 + lane] = l;
+  } else if (qi < length) {
     const int b = bh / heads, h = bh - b * heads;
     uint16_t* orow = o + b * o_batch_stride + h * o_head_stride + (int64_t)qi * o_row_stride;
 #pragma unroll
@@ -361,29 +397,86 @@ __global__ __launch_bounds__(kThreads, 2) void attend_kernel(
   }
 }
 
+// Sums the split partials in split order and writes O = bf16(acc / l) with attend_kernel's
+// own epilogue arithmetic.  Thread id = ((unit * 8 + wave) * 16 + i) * 64 + lane takes one
+// register group of one lane, so split s's value is float4 s * units * 8192 + id: every
+// split is one contiguous 16-byte load per thread.
+constexpr int kMergeThreads = 256;
+
+__global__ __launch_bounds__(kMergeThreads) void attend_merge_kernel(
+    const float* __restrict__ part_acc, const float* __restrict__ part_l, uint16_t* __restrict__ o,
+    int length, int q_blocks, int64_t units, int heads, int splits, int64_t o_batch_stride,
+    int64_t o_head_stride, int64_t o_row_stride) {
+  const int64_t id = (int64_t)blockIdx.x * kMergeThreads + threadIdx.x;
+  const int lane = (int)(id & 63);
+  const int i = (int)((id >> 6) & 15);
+  const int64_t wave_slot = id >> 10;            // unit * 8 + wave
+  const int wave = (int)(wave_slot & 7);
+  const int64_t unit = wave_slot >> 3;
+  if (unit >= units) return;
+  const int64_t bh = unit / q_blocks;
+  const int qblk = (int)(unit - bh * q_blocks);
+  const int qi = qblk * kBM + wave * 32 + (lane & 31);
+  if (qi >= length) return;
+  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  float l = 0.0f;
+#pragma unroll 4
+  for (int s = 0; s < splits; ++s) {
+    acc += reinterpret_cast<const f32x4*>(part_acc)[s * units * 8192 + id];
+    l += part_l[(s * units + unit) * 512 + wave * 64 + lane];
+  }
+  const int64_t b = bh / heads, h = bh - b * heads;
+  const int d0 = (i >> 2) * 32 + (i & 3) * 8 + (lane >> 5) * 4;
+  uint2 val;
+  val.x = flk::pack_bf16x2(acc.x / l, acc.y / l);
+  val.y = flk::pack_bf16x2(acc.z / l, acc.w / l);
+  *reinterpret_cast<uint2*>(o + b * o_batch_stride + h * o_head_stride + (int64_t)qi * o_row_stride + d0) = val;
+}
+
 }  // namespace
 
 namespace {
 
-int launch_attend(const void* q, const void* k, const void* v, void* o, int batch, int heads, int length,
-                  int head_dim, int64_t o_batch_stride, int64_t o_head_stride, int64_t o_row_stride,
-                  void* stream) {
+// Blocks per launch below which the key range is split: a grid this small leaves CUs idle
+// for the whole launch (256 CUs, one block each).
+constexpr int kSplitBelow = 192;
+constexpr int kCUs = 256;
+
+// Argument checks shared by the entry points: FLK_OK = launch, kNothing = empty input (nothing
+// to do), else an error status.
+constexpr int kNothing = 1;
+
+int check_attend(const void* q, const void* k, const void* v, void* o, int batch, int heads, int length,
+                 int head_dim, int64_t o_batch_stride, int64_t o_head_stride, int64_t o_row_stride) {
   if (head_dim != kD) return FLK_E_UNSUPPORTED;
   if (batch < 0 || heads < 0 || length < 0) return FLK_E_INVALID;
-  if (batch == 0 || heads == 0 || length == 0) return FLK_OK;
+  if (batch == 0 || heads == 0 || length == 0) return kNothing;
   if (!q || !k || !v || !o) return FLK_E_INVALID;
   if (!flk_host_aligned(q, 16) || !flk_host_aligned(k, 16) || !flk_host_aligned(v, 16) ||
       !flk_host_aligned(o, 8) || o_batch_stride % 4 || o_head_stride % 4 || o_row_stride % 4)
     return FLK_E_ALIGN;
   if (o_batch_stride < 0 || o_head_stride < 0 || o_row_stride < kD) return FLK_E_INVALID;
-  const int64_t q_blocks = (length + kBM - 1) / kBM;
-  const int64_t total = q_blocks * batch * heads;
-  if (total > INT32_MAX) return FLK_E_INVALID;
-  hipLaunchKernelGGL(attend_kernel, dim3((unsigned)total), dim3(kThreads), 0,
+  if ((int64_t)((length + kBM - 1) / kBM) * batch * heads > INT32_MAX) return FLK_E_INVALID;
+  return FLK_OK;
+}
+
+int64_t q_tiles(int length) { return (length + kBM - 1) / kBM; }
+int key_groups(int length) { return ((length + kBN - 1) / kBN + 3) / 4; }
+
+// Workspace of a split launch: per split and (b, h, 256-query tile), 512 lanes x (64 acc + 1 l)
+// floats.
+int64_t split_workspace_bytes(int batch, int heads, int length, int splits) {
+  return (int64_t)splits * batch * heads * q_tiles(length) * kThreads * 65 * (int64_t)sizeof(float);
+}
+
+int launch_attend(const void* q, const void* k, const void* v, void* o, int batch, int heads, int length,
+                  int64_t o_batch_stride, int64_t o_head_stride, int64_t o_row_stride, void* stream) {
+  const int64_t total = q_tiles(length) * batch * heads;
+  hipLaunchKernelGGL(attend_kernel<false>, dim3((unsigned)total), dim3(kThreads), 0,
                      static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(q),
                      static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
-                     static_cast<uint16_t*>(o), length, (int)q_blocks, (int)total, heads, o_batch_stride,
-                     o_head_stride, o_row_stride);
+                     static_cast<uint16_t*>(o), length, (int)q_tiles(length), (int)total, heads, 1,
+                     o_batch_stride, o_head_stride, o_row_stride, nullptr, nullptr);
   return flk_launch_status();
 }
 
@@ -391,13 +484,64 @@ int launch_attend(const void* q, const void* k, const void* v, void* o, int batc
 
 extern "C" int flk_attend(const void* q, const void* k, const void* v, void* o, int batch,
                           int heads, int length, int head_dim, void* stream) {
-  const int64_t row = kD, head = (int64_t)length * kD;
-  return launch_attend(q, k, v, o, batch, heads, length, head_dim, (int64_t)heads * head, head, row, stream);
+  const int64_t row = kD, head = (int64_t)length * kD, bstride = (int64_t)heads * head;
+  const int st = check_attend(q, k, v, o, batch, heads, length, head_dim, bstride, head, row);
+  if (st != FLK_OK) return st == kNothing ? FLK_OK : st;
+  return launch_attend(q, k, v, o, batch, heads, length, bstride, head, row, stream);
 }
 
 extern "C" int flk_attend_to(const void* q, const void* k, const void* v, void* o, int batch, int heads,
                              int length, int head_dim, int64_t o_batch_stride, int64_t o_head_stride,
                              int64_t o_row_stride, void* stream) {
-  return launch_attend(q, k, v, o, batch, heads, length, head_dim, o_batch_stride, o_head_stride, o_row_stride,
-                       stream);
+  const int st = check_attend(q, k, v, o, batch, heads, length, head_dim, o_batch_stride, o_head_stride,
+                              o_row_stride);
+  if (st != FLK_OK) return st == kNothing ? FLK_OK : st;
+  return launch_attend(q, k, v, o, batch, heads, length, o_batch_stride, o_head_stride, o_row_stride, stream);
+}
+
+extern "C" int flk_attend_plan(int batch, int heads, int length, int* splits, int64_t* workspace_bytes) {
+  if (batch < 0 || heads < 0 || length < 0 || !splits || !workspace_bytes) return FLK_E_INVALID;
+  int s = 1;
+  const int64_t blocks = q_tiles(length) * batch * heads;
+  if (blocks > 0 && blocks < kSplitBelow) {
+    // As many splits as fill the CUs once, each keeping at least two 4-tile key groups.
+    s = (int)std::min<int64_t>(kCUs / blocks, key_groups(length) / 2);
+    s = std::max(s, 1);
+  }
+  *splits = s;
+  *workspace_bytes = s > 1 ? split_workspace_bytes(batch, heads, length, s) : 0;
+  return FLK_OK;
+}
+
+extern "C" int flk_attend_split_to(const void* q, const void* k, const void* v, void* o, int batch, int heads,
+                                   int length, int head_dim, int64_t o_batch_stride, int64_t o_head_stride,
+                                   int64_t o_row_stride, int splits, void* workspace, int64_t workspace_bytes,
+                                   void* stream) {
+  const int st = check_attend(q, k, v, o, batch, heads, length, head_dim, o_batch_stride, o_head_stride,
+                              o_row_stride);
+  if (st != FLK_OK) return st == kNothing ? FLK_OK : st;
+  if (splits < 1 || splits > key_groups(length)) return FLK_E_INVALID;
+  if (splits == 1) return launch_attend(q, k, v, o, batch, heads, length, o_batch_stride, o_head_stride,
+                                        o_row_stride, stream);
+  const int64_t need = split_workspace_bytes(batch, heads, length, splits);
+  if (!workspace || workspace_bytes < need) return FLK_E_INVALID;
+  if (!flk_host_aligned(workspace, 16)) return FLK_E_ALIGN;
+  const int64_t units = q_tiles(length) * batch * heads;
+  const int64_t total = units * splits;
+  if (total > INT32_MAX) return FLK_E_INVALID;
+  float* part_acc = static_cast<float*>(workspace);
+  float* part_l = part_acc + total * kThreads * 64;
+  const hipStream_t hs = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(attend_kernel<true>, dim3((unsigned)total), dim3(kThreads), 0, hs,
+                     static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
+                     static_cast<const uint16_t*>(v), static_cast<uint16_t*>(o), length, (int)q_tiles(length),
+                     (int)total, heads, splits, o_batch_stride, o_head_stride, o_row_stride, part_acc, part_l);
+  const int launched = flk_launch_status();
+  if (launched != FLK_OK) return launched;
+  const int64_t merge_blocks = units * kWaves * 16 * 64 / kMergeThreads;
+  if (merge_blocks > INT32_MAX) return FLK_E_INVALID;
+  hipLaunchKernelGGL(attend_merge_kernel, dim3((unsigned)merge_blocks), dim3(kMergeThreads), 0, hs, part_acc,
+                     part_l, static_cast<uint16_t*>(o), length, (int)q_tiles(length), units, heads, splits,
+                     o_batch_stride, o_head_stride, o_row_stride);
+  return flk_launch_status();
 }

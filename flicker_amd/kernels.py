@@ -218,9 +218,14 @@ def logit_bound(q_scale, k_scale):
 
 
 def attend(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, block: int | None = None,
-           interpret: bool = False, out: torch.Tensor | None = None) -> torch.Tensor:
+           interpret: bool = False, out: torch.Tensor | None = None,
+           splits: int | None = None) -> torch.Tensor:
     """kernels.py:105-145 -- bounded flash attention (no running max), q pre-scaled by
-    1/sqrt(D).  q, k, v (B, H, L, D) bf16 -> o (B, H, L, D) bf16."""
+    1/sqrt(D).  q, k, v (B, H, L, D) bf16 -> o (B, H, L, D) bf16.
+
+    Grids too small to fill the GPU (few heads or short sequences) cut the keys into ranges
+    whose partial sums are added afterwards (flk_attend_split_to); ``splits`` overrides the
+    automatic choice (1 = never split)."""
     if interpret:
         raise ValueError("interpret=True is Pallas' CPU emulation; flicker_amd has one HIP path")
     for name, t in (("q", q), ("k", k), ("v", v)):
@@ -244,12 +249,12 @@ def attend(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, block: int | No
         out = torch.empty_like(q)
     elif out.shape != q.shape or out.dtype != torch.bfloat16 or not out.is_contiguous():
         raise ValueError("out must be a contiguous bf16 tensor shaped like q")
-    _launch_attend(q, k, v, out)
+    _launch_attend(q, k, v, out, (heads * length * dim, length * dim, dim), splits)
     return out
 
 
 def attend_merged(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
-                  out: torch.Tensor | None = None) -> torch.Tensor:
+                  out: torch.Tensor | None = None, splits: int | None = None) -> torch.Tensor:
     """``merge_heads(attend(q, k, v))`` (modules.py:63-65 after kernels.py:105-145) in one
     kernel: the attention epilogue writes o[b, t, h*D:(h+1)*D] directly, so the transposing
     copy of merge_heads disappears.  q, k, v (B, H, L, D) bf16 -> (B, L, H*D) bf16; ``out`` may
@@ -274,12 +279,23 @@ def attend_merged(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
         raise ValueError(f"out must be a bf16 ({batch}, {length}, {heads * dim}) view with contiguous, "
                          "4-element aligned rows")
     _on_gpu("out", out)
-    _lib.run("flk_attend_to", (q, k, v, out), q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
-             batch, heads, length, dim, out.stride(0), dim, out.stride(1), _lib.stream_of(q))
+    _launch_attend(q, k, v, out, (out.stride(0), dim, out.stride(1)), splits)
     return out
 
 
-def _launch_attend(q, k, v, out) -> None:
+def _launch_attend(q, k, v, out, o_strides, splits: int | None) -> None:
+    """O through strides (batch, head, row); the key-split path when the grid is small."""
     batch, heads, length, dim = q.shape
-    _lib.run("flk_attend", (q, k, v, out), q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
-             batch, heads, length, dim, _lib.stream_of(q))
+    planned, _ = _lib.attend_plan(batch, heads, length)
+    splits = planned if splits is None else int(splits)
+    groups = max(1, -(-length // 256))
+    if not 1 <= splits <= groups:
+        raise ValueError(f"splits must be in [1, {groups}] for L={length}, got {splits}")
+    args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), batch, heads, length, dim, *o_strides)
+    if splits == 1:
+        _lib.run("flk_attend_to", (q, k, v, out), *args, _lib.stream_of(q))
+        return
+    nbytes = splits * batch * heads * groups * 512 * 65 * 4
+    workspace = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
+    _lib.run("flk_attend_split_to", (q, k, v, out, workspace), *args, splits, workspace.data_ptr(), nbytes,
+             _lib.stream_of(q))

@@ -96,6 +96,38 @@ int flk_attend_to(const void* q, const void* k, const void* v, void* o,
                   int64_t o_batch_stride, int64_t o_head_stride, int64_t o_row_stride, void* stream);
 
 /*
+ * flk_attend_to for grids too small to fill the GPU (few heads: one GPU's share of a
+ * head-parallel run, or short sequences).  It computes the same attend (src/flicker/
+ * kernels.py:105-145), with the keys cut into `splits` ranges of whole 256-key groups.
+ * Each (b, h, 256-query tile, range) block sums its own acc and l.  A second kernel adds the
+ * ranges in order, as plain sums: the reference keeps no running max, so no rescaling is
+ * needed.  It then writes o = bf16(acc / l).
+ *
+ * Only the f32 summation order differs from flk_attend_to.  Results are deterministic for
+ * a given (batch, heads, length, splits).
+ *
+ * Arguments:
+ * - 1 <= splits <= ceil(length / 256); splits == 1 is flk_attend_to itself.
+ * - `workspace`: caller-owned, 16-byte aligned scratch of at least
+ *   splits * batch * heads * ceil(length / 256) * 512 * 65 * 4 bytes (f32 partial acc
+ *   and l of every 256-query tile).  Nothing in it needs to be initialised; it is dead
+ *   after the call.
+ * - Other arguments as flk_attend_to.
+ */
+int flk_attend_split_to(const void* q, const void* k, const void* v, void* o,
+                        int batch, int heads, int length, int head_dim,
+                        int64_t o_batch_stride, int64_t o_head_stride, int64_t o_row_stride,
+                        int splits, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * The split count flk_attend_split_to should use for a shape, and its workspace size.
+ * *splits = 1 (workspace 0) when the plain grid already has >= 192 blocks of 256 queries.
+ * Otherwise it takes as many ranges as fill the 256 CUs once, keeping at least 512 keys per
+ * range.  A pure function of its arguments; no device work.
+ */
+int flk_attend_plan(int batch, int heads, int length, int* splits, int64_t* workspace_bytes);
+
+/*
  * RoPE angle tables.  Replaces rope.embed_nd / rope.rope_freqs (src/flicker/rope.py:9-21):
  *   ids  (length, n_axes) float32 positions, row t at t*ids_row_stride floats
  *   axes_dim  host array of n_axes even ints (1 <= n_axes <= 8)

@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 import torch
 
-from flicker_amd import kernels
+from flicker_amd import _lib, kernels
 from oracle import path as P
 from tests._util import abs_stats, describe, to_np
 
@@ -33,10 +33,12 @@ def prepped_case(batch, heads, length, seed, scale=1.0):
     return q, k, v
 
 
-def run_attend(q, k, v, device):
+def run_attend(q, k, v, device, splits=None):
+    """Launch below kernels.attend's score-tile check, so any L can be tested; splits=None
+    takes flk_attend_plan's choice (the key-split path on small grids)."""
     q, k, v = (t.to(device) for t in (q, k, v))
     out = torch.empty_like(q)
-    kernels._launch_attend(q.contiguous(), k.contiguous(), v.contiguous(), out)
+    kernels._launch_attend(q.contiguous(), k.contiguous(), v.contiguous(), out, out.stride()[:3], splits)
     torch.cuda.synchronize()
     return to_np(out)
 
@@ -126,3 +128,57 @@ def test_attend_merged_equals_merge_heads_of_attend(device, batch, heads, length
     torch.cuda.synchronize()
     assert torch.equal(wide[..., 32:32 + heads * D].view(torch.int16), want.view(torch.int16))
     assert bool((wide[..., :32] == 7.0).all()) and bool((wide[..., 32 + heads * D:] == 7.0).all())
+
+
+@pytest.mark.parametrize("batch,heads,length,splits", [
+    (1, 3, 4608, None), (1, 3, 4608, 2), (1, 2, 4352, None), (2, 3, 1536, 3), (1, 1, 1000, 4),
+    (1, 1, 513, 3),
+])
+def test_attend_key_split_matches_oracle(device, batch, heads, length, splits):
+    """The key-split path (flk_attend_split_to): each range's partial acc and l, then their
+    plain sums -- the same gate as the one-pass kernel, and within rounding of it."""
+    planned, _ = _lib.attend_plan(batch, heads, length)
+    if splits is None:
+        assert planned > 1, "the shape is meant to take the split path"
+    q, k, v = prepped_case(batch, heads, length, seed=length + 3)
+    got = run_attend(q, k, v, device, splits)
+    want = P.attend_bounded(to_np(q), to_np(k), to_np(v))
+    tight_gate(f"split {splits or planned} B{batch} H{heads} L{length}", got, want)
+    one = run_attend(q, k, v, device, 1)
+    diff = np.abs(got.astype(np.float64) - one)
+    assert np.all(diff <= 2 * np.abs(one) * 2.0 ** -8 + 1e-6)   # one bf16 ulp of either value
+    assert np.mean(diff > 0) <= 0.01
+
+
+def test_attend_key_split_dominant_key_in_last_range(device):
+    """A key near the end (the last of 4 ranges) at logit ~ 60 outweighs the others, so the
+    merged output is its value row: the ranges' l and acc must be summed, not overwritten."""
+    length = 2048
+    q = torch.zeros(1, 1, length, D)
+    q[..., 0] = 60.0 / math.sqrt(D) / 4
+    k = torch.zeros(1, 1, length, D)
+    k[:, :, 1900, 0] = 4 * math.sqrt(D)
+    v = torch.randn(1, 1, length, D, generator=torch.Generator().manual_seed(9))
+    q, k, v = (t.to(torch.bfloat16) for t in (q, k, v))
+    got = run_attend(q, k, v, device, 4)
+    st = abs_stats(got, np.broadcast_to(to_np(v)[:, :, 1900:1901], got.shape))
+    print(describe("split dominant key", st))
+    assert st["max_abs"] <= 1e-2
+    # uniform keys across ranges: o = mean(v) over all 2048 keys
+    ku = torch.zeros(1, 1, length, D).to(torch.bfloat16)
+    got = run_attend(q, ku, v, device, 4)
+    mean_v = to_np(v).astype(np.float64).mean(axis=2, keepdims=True)
+    assert abs_stats(got, np.broadcast_to(mean_v, got.shape))["max_abs"] <= 2e-3
+
+
+def test_attend_merged_key_split(device):
+    """attend_merged on the split path writes exactly merge_heads of the split attend."""
+    from flicker_amd import modules
+    q, k, v = (t.to(device) for t in prepped_case(1, 3, 4608, seed=21))
+    assert _lib.attend_plan(1, 3, 4608)[0] > 1
+    want = modules.merge_heads(kernels.attend(q, k, v))
+    got = kernels.attend_merged(q, k, v)
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+    with pytest.raises(ValueError):
+        kernels.attend(q, k, v, splits=19)     # more ranges than 256-key groups

@@ -57,7 +57,7 @@ def test_attend_golden(device):
     g = load("attn.npz")
     q, k, v = (bf16_tensor(g[n], device)[None] for n in ("q_pre", "k", "v"))
     o = torch.empty_like(q)
-    kernels._launch_attend(q.contiguous(), k.contiguous(), v.contiguous(), o)
+    kernels._launch_attend(q.contiguous(), k.contiguous(), v.contiguous(), o, o.stride()[:3], None)
     torch.cuda.synchronize()
     want = g["bounded"].astype(np.float64)
     diff = np.abs(to_np(o)[0] - want)

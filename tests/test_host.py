@@ -64,6 +64,30 @@ def test_attend_validation(lib):
     assert g(FAKE, FAKE, FAKE, FAKE, 1, 24, 4608, 64, 4608 * hd, 128, hd, None) == _lib.FLK_E_UNSUPPORTED
 
 
+def test_attend_split_plan_and_validation(lib):
+    """flk_attend_plan splits only grids below 192 blocks of 256 queries, into as many key
+    ranges as fill 256 CUs once with at least 512 keys each; flk_attend_split_to rejects bad
+    split counts and short or misaligned workspaces before launching anything."""
+    cases = {(1, 24, 4608): 1, (1, 12, 4608): 1, (1, 24, 1536): 1, (1, 6, 4608): 2, (1, 3, 4608): 4,
+             (1, 1, 4608): 9, (1, 2, 257): 1, (1, 1, 64): 1, (0, 3, 4608): 1}
+    for (b, h, length), want in cases.items():
+        splits, nbytes = _lib.attend_plan(b, h, length)
+        assert splits == want, (b, h, length, splits)
+        assert nbytes == (splits * b * h * -(-length // 256) * 512 * 65 * 4 if splits > 1 else 0)
+    f = lib.flk_attend_split_to
+    hd, need = 3 * 128, 4 * 3 * 18 * 512 * 65 * 4
+    args = (FAKE, FAKE, FAKE, FAKE, 1, 3, 4608, 128, 4608 * hd, 128, hd)
+    assert f(*args, 0, FAKE, need, None) == _lib.FLK_E_INVALID           # no ranges
+    assert f(*args, 19, FAKE, 10 ** 9, None) == _lib.FLK_E_INVALID       # more ranges than key groups
+    assert f(*args, 4, FAKE, need - 1, None) == _lib.FLK_E_INVALID       # short workspace
+    assert f(*args, 4, None, need, None) == _lib.FLK_E_INVALID
+    assert f(*args, 4, FAKE + 4, need, None) == _lib.FLK_E_ALIGN
+    assert f(FAKE, FAKE, FAKE, FAKE, 1, 0, 4608, 128, 0, 128, hd, 4, None, 0, None) == _lib.FLK_OK   # empty
+    with pytest.raises(_lib.HipKernelError):
+        _lib.check(lib.flk_attend_plan(1, -1, 10, ctypes.byref(ctypes.c_int()), ctypes.byref(ctypes.c_int64())),
+                   "flk_attend_plan")
+
+
 def test_qk_prep_validation(lib):
     f = lib.flk_qk_prep
     args = dict(qkv=FAKE, bs=4608 * 9216, rs=9216, cos=FAKE, sin=FAKE, ts=128, qs=FAKE, ks=FAKE, f32=0,
