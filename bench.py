@@ -11,7 +11,9 @@ average launch duration: `value` is attend's TFLOP/s from that, and the line als
 qk_prep's GB/s and both roofline fractions.  To keep the QKV input from being
 served by the 256 MB Infinity Cache between steps, steps rotate over buffer sets
 whose total exceeds it.  A CPU baseline (the torch-CPU restatement of the reference's
-plain-XLA path, the oracle) is timed on the host cores.
+plain-XLA path, the oracle) is timed on the host cores.  `head_share` times attend on one
+GPU's share of an 8-way head-parallel run (3 of the 24 heads, the full sequence), the grid
+that the key-split path exists for.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload klein_1024]
 
@@ -188,6 +190,29 @@ def projection_operands(p, dev):
     qw = w8a8.quantize_linear(wt, w8a8.absmax_cols(x))
     xq, a_scale = w8a8.quantize_act(x, qw.inv_smooth)
     return x, qw, xq, a_scale
+
+
+SHARE_GPUS = 8
+
+
+def head_share_leg(w, qkv_heads, timed) -> dict:
+    """attend on one GPU's share of a head-parallel run over SHARE_GPUS GPUs (heads / 8 of
+    them, full sequence): the grid is then too small to fill the GPU, so kernels.attend takes
+    its key-split path.  Timed as planned and with the split off."""
+    import torch
+    from flicker_amd import _lib, kernels
+    heads = w.num_heads // SHARE_GPUS
+    q, k, v = (t[:, :heads].contiguous() for t in qkv_heads)
+    o = torch.empty_like(q)
+    splits, _ = _lib.attend_plan(w.batch, heads, w.length)
+    flops = 4 * w.batch * heads * w.length * w.length * w.head_dim
+    for _ in range(20):
+        kernels.attend(q, k, v, out=o)
+    split_ms = timed(lambda i: kernels.attend(q, k, v, out=o), 200)
+    plain_ms = timed(lambda i: kernels.attend(q, k, v, out=o, splits=1), 200)
+    return {"heads": heads, "of_gpus": SHARE_GPUS, "splits": splits, "avg_launch_us": round(split_ms * 1e3, 2),
+            "achieved": round(flops / (split_ms * 1e-3) / 1e12, 1), "unit": "TFLOP/s",
+            "unsplit_us": round(plain_ms * 1e3, 2)}
 
 
 def w8a8_leg(args, timed, dev) -> dict:
@@ -441,6 +466,8 @@ def main() -> int:
         result["qk_prep"]["position_ids"] = {
             "avg_launch_us": round(qk_ids_ms * 1e3, 2), "bytes_per_launch": w.qk_prep_bytes(tables=False),
             "achieved": round(ids_gbs, 1), "unit": "GB/s", "frac": round(ids_gbs / HBM_PEAK_GBS, 4)}
+    if args.only == "step" and w.num_heads % SHARE_GPUS == 0:
+        result["head_share"] = head_share_leg(w, sets[0][1], timed)
     if not args.no_w8a8 and args.only == "step":
         result["w8a8"] = w8a8_leg(args, timed, dev)
         proj = workloads.PROJECTIONS[args.projection]
