@@ -122,3 +122,38 @@ def test_graph_replay_int8_projection(device):
         eager = w8a8.linear(fresh, qw)
         torch.cuda.synchronize()
         assert torch.equal(replayed, eager), f"replay with input seed {seed} differs from eager"
+
+
+def test_graph_replay_attend_key_split(device):
+    """The key-split path inside a graph: its workspace comes from torch's allocator during
+    capture (the graph's own pool), and every replay equals the eager split result."""
+    from flicker_amd import _lib
+    heads, length = 3, 2048
+    assert _lib.attend_plan(1, heads, length)[0] > 1
+
+    def qkv_of(seed):
+        g = torch.Generator().manual_seed(seed)
+        x = torch.randn(3, 1, heads, length, D, generator=g)
+        x = x / x.pow(2).mean(-1, keepdim=True).sqrt()
+        return (x[0] / math.sqrt(D)).to(torch.bfloat16), x[1].to(torch.bfloat16), x[2].to(torch.bfloat16)
+
+    static = tuple(t.to(device) for t in qkv_of(10))
+    static_o = torch.empty_like(static[0])
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        kernels.attend(*static, out=static_o)      # warm-up outside the capture
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        kernels.attend(*static, out=static_o)
+    for seed in (11, 12, 13):
+        fresh = tuple(t.to(device) for t in qkv_of(seed))
+        for dst, src in zip(static, fresh):
+            dst.copy_(src)
+        graph.replay()
+        torch.cuda.synchronize()
+        replayed = static_o.clone()
+        eager = kernels.attend(*fresh)                # eager split work between replays
+        torch.cuda.synchronize()
+        assert torch.equal(replayed, eager), f"replay with input seed {seed} differs from eager"
