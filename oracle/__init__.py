@@ -4,8 +4,8 @@ This package restates, on the CPU, what kelechi-c/flicker computes on its
 attention hot path, so that the HIP kernels in ``flicker_amd`` can be checked
 against it.  It is never part of the product: only ``tests/``,
 ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
-import it, and only as the checker (or, for the baseline, as the timed CPU
-restatement of the reference's plain-XLA path).
+import it, and only to compare results against it (or, for the baseline, as
+the timed CPU restatement of the reference's plain-XLA path).
 
 Modules
   numerics   bf16 round-to-nearest-even on float32 arrays
