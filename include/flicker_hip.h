@@ -23,7 +23,7 @@ extern "C" {
 #define FLK_OK 0
 #define FLK_E_INVALID (-1)     /* a size, count or offset out of range          */
 #define FLK_E_ALIGN (-2)       /* a pointer or stride breaks the 16-byte rule    */
-#define FLK_E_UNSUPPORTED (-3) /* a shape this build has no kernel for          */
+#define FLK_E_UNSUPPORTED (-3) /* a shape the library has no kernel for        */
 
 /* ABI revision of this header (bumped on any signature change). */
 int flk_abi_version(void);
