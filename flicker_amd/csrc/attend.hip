@@ -240,16 +240,17 @@ __global__ __launch_bounds__(kThreads, 2) void attend_kernel(
   __shared__ __attribute__((aligned(1024))) uint8_t smem[kSmemBytes];
 
   // XCD-aware renumbering: hardware block id p runs on XCD p % 8; give each XCD a
-  // contiguous range of logical ids (head-major, then split, then query tile), so the
-  // query tiles that read one head's keys share an L2.
+  // contiguous range of logical ids (head-major, then query tile, then key range), so the
+  // blocks that read one head's keys share an L2, and so do the key ranges of one query
+  // tile, whose partials attend_merge_kernel then reads on the same XCD.
   const int p = blockIdx.x;
   const int xcd = p % kXcds, local = p / kXcds;
   const int per = total_blocks / kXcds, extra = total_blocks % kXcds;
   const int logical = xcd * per + min(xcd, extra) + local;
-  const int qblk = logical % q_blocks;
-  const int rest = logical / q_blocks;
-  const int split = kSplit ? rest % splits : 0;
-  const int bh = kSplit ? rest / splits : rest;
+  const int split = kSplit ? logical % splits : 0;
+  const int rest = kSplit ? logical / splits : logical;
+  const int qblk = rest % q_blocks;
+  const int bh = rest / q_blocks;
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
@@ -400,14 +401,18 @@ __global__ __launch_bounds__(kThreads, 2) void attend_kernel(
 // Sums the split partials in split order and writes O = bf16(acc / l) with attend_kernel's
 // own epilogue arithmetic.  Thread id = ((unit * 8 + wave) * 16 + i) * 64 + lane takes one
 // register group of one lane, so split s's value is float4 s * units * 8192 + id: every
-// split is one contiguous 16-byte load per thread.
+// split is one contiguous 16-byte load per thread.  Blocks are renumbered like
+// attend_kernel's, so unit u is merged on the XCD whose L2 holds its partials.
 constexpr int kMergeThreads = 256;
 
 __global__ __launch_bounds__(kMergeThreads) void attend_merge_kernel(
     const float* __restrict__ part_acc, const float* __restrict__ part_l, uint16_t* __restrict__ o,
     int length, int q_blocks, int64_t units, int heads, int splits, int64_t o_batch_stride,
     int64_t o_head_stride, int64_t o_row_stride) {
-  const int64_t id = (int64_t)blockIdx.x * kMergeThreads + threadIdx.x;
+  const int p = blockIdx.x;
+  const int xcd = p % kXcds, local = p / kXcds;
+  const int per = gridDim.x / kXcds, extra = gridDim.x % kXcds;
+  const int64_t id = (int64_t)(xcd * per + min(xcd, extra) + local) * kMergeThreads + threadIdx.x;
   const int lane = (int)(id & 63);
   const int i = (int)((id >> 6) & 15);
   const int64_t wave_slot = id >> 10;            // unit * 8 + wave
