@@ -204,7 +204,7 @@ struct Ctx {
   CopyPlan cp;
 };
 
-// Iteration t at ring position r = t % 4: the exp work of units 2t and 2t+1.  It reads K
+// Iteration t at ring position r = (t - t_begin) % 4: the exp work of units 2t and 2t+1.  It reads K
 // tiles t and t+1 and V tiles t-1 and t, and starts the copies of K tile t+3 and V tile
 // t+2 into the slots of K tile t-1 and V tile t-2, which no read of this iteration touches.
 // Called with a literal r in the unrolled main loop, so every LDS address folds to a
@@ -227,9 +227,10 @@ __device__ __forceinline__ void iteration(WaveState& w, const Ctx& c, int t, int
 }
 
 // kSplit = false: the block takes every key of its 256 queries and writes O.
-// kSplit = true: the keys are cut into `splits` ranges of whole 4-tile groups (so ring
-// positions stay literal in the unrolled loop); the block takes one range and writes its
-// unnormalised acc and l to part_acc / part_l, which attend_merge_kernel sums.  Without a
+// kSplit = true: the key tiles are cut into `splits` ranges of equal length (+-1 tile); the
+// block takes one range and writes its unnormalised acc and l to part_acc / part_l, which
+// attend_merge_kernel sums.  Ring slots count from the block's first tile, so the unrolled
+// loop keeps literal ring positions wherever the range starts.  Without a
 // running max the partial sums of different key ranges add as they are.
 template <bool kSplit>
 __global__ __launch_bounds__(kThreads, 2) void attend_kernel(
@@ -263,9 +264,8 @@ __global__ __launch_bounds__(kThreads, 2) void attend_kernel(
   c.cp.last_tile = c.ntiles - 1;
   int t_begin = 0, t_end = c.ntiles;   // this block's key tiles
   if constexpr (kSplit) {
-    const int groups = (c.ntiles + 3) / 4;
-    t_begin = 4 * (split * groups / splits);
-    t_end = min(4 * ((split + 1) * groups / splits), c.ntiles);
+    t_begin = split * c.ntiles / splits;
+    t_end = (split + 1) * c.ntiles / splits;
   }
   c.cp.lds_wave_off = __builtin_amdgcn_readfirstlane(wave * kRowsPerWave * kRowBytes);
   {
@@ -284,8 +284,8 @@ __global__ __launch_bounds__(kThreads, 2) void attend_kernel(
   c.kh = k + head_off;
   c.vh = v + head_off;
 
-  // Prologue copies: K tiles t_begin .. +2, V tiles t_begin .. +1 (ring slots 0-2 and 0-1:
-  // t_begin is a multiple of 4).
+  // Prologue copies: K tiles t_begin .. +2, V tiles t_begin .. +1 into ring slots 0-2 and 0-1
+  // (tile t sits in slot (t - t_begin) % 4).
   for (int tl = 0; tl < 3; ++tl) copy_tile(smem + tl * kTileBytes, c.kh, t_begin + tl, c.cp);
   for (int tl = 0; tl < 2; ++tl) copy_tile(smem + kVRing + tl * kTileBytes, c.vh, t_begin + tl, c.cp);
 
@@ -348,13 +348,13 @@ __global__ __launch_bounds__(kThreads, 2) void attend_kernel(
     iteration<false>(w, c, t + 2, 2);
     iteration<false>(w, c, t + 3, 3);
   }
-  for (; t < t_end; ++t) iteration<true>(w, c, t, t & 3);
+  for (; t < t_end; ++t) iteration<true>(w, c, t, (t - t_begin) & 3);
   // No copy may still be writing this block's LDS when the block ends.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   // Drain: O^T += V(U-1)^T P(U-1)^T for the last unit (unit 1 of the last tile).
   {
-    const uint8_t* v_last = smem + kVRing + ((t_end - 1) & 3) * kTileBytes + kUnitBytes;
+    const uint8_t* v_last = smem + kVRing + ((t_end - 1 - t_begin) & 3) * kTileBytes + kUnitBytes;
     const bf16x8 pb0 = __builtin_bit_cast(bf16x8, make_uint4(w.pB[0], w.pB[1], w.pB[2], w.pB[3]));
     const bf16x8 pb1 = __builtin_bit_cast(bf16x8, make_uint4(w.pB[4], w.pB[5], w.pB[6], w.pB[7]));
 #pragma unroll

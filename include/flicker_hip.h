@@ -98,7 +98,8 @@ int flk_attend_to(const void* q, const void* k, const void* v, void* o,
 /*
  * flk_attend_to for grids too small to fill the GPU (few heads: one GPU's share of a
  * head-parallel run, or short sequences).  It computes the same attend (src/flicker/
- * kernels.py:105-145), with the keys cut into `splits` ranges of whole 256-key groups.
+ * kernels.py:105-145), with the keys cut into `splits` ranges of equal length (in 64-key
+ * tiles, +-1 tile).
  * Each (b, h, 256-query tile, range) block sums its own acc and l.  A second kernel adds the
  * ranges in order, as plain sums: the reference keeps no running max, so no rescaling is
  * needed.  It then writes o = bf16(acc / l).
