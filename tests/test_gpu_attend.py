@@ -182,3 +182,18 @@ def test_attend_merged_key_split(device):
     assert torch.equal(got.view(torch.int16), want.view(torch.int16))
     with pytest.raises(ValueError):
         kernels.attend(q, k, v, splits=19)     # more ranges than 256-key groups
+
+
+def test_attend_key_split_long_sequence_matches_unsplit(device):
+    """2048^2 Klein length (L = 16896) on one head: 66 query tiles plan 3 key ranges of 88
+    tiles.  Too long for the oracle, so the split path is held to the one-pass kernel: the
+    same sums in another f32 order, so at most one bf16 ulp apart on a few elements."""
+    length = 16896
+    planned, _ = _lib.attend_plan(1, 1, length)
+    assert planned == 3
+    q, k, v = prepped_case(1, 1, length, seed=31)
+    split = run_attend(q, k, v, device)
+    one = run_attend(q, k, v, device, 1)
+    diff = np.abs(split.astype(np.float64) - one)
+    assert np.all(diff <= 2 * np.abs(one) * 2.0 ** -8 + 1e-6)
+    assert np.mean(diff > 0) <= 0.01
