@@ -45,6 +45,11 @@
 // Blocks of 8 waves (two per SIMD) take 256 queries of one (b, h).  Blocks are renumbered
 // so that all query tiles of one head run on the same XCD (hardware deals blocks
 // round-robin over the 8 XCDs), keeping the head's K/V in one L2.
+//
+// Small grids (few heads, short sequences) leave CUs idle for the whole launch.  For them
+// the keys are cut into ranges (flk_attend_split_to): each block sums one range into
+// unnormalised (acc, l) partials, and attend_merge_kernel adds the ranges in order and
+// divides.  With no running max the partial sums need no rescaling.
 
 #include <algorithm>
 
