@@ -21,8 +21,9 @@
 //
 // The RoPE lanes come from one of two sources: the (L, 128) f32 cos / sin tables
 // (kernels.py:28-31), or -- flk_qk_prep_ids -- the token's position ids, from which each
-// lane computes the cos / sin of its 4 pairs (rope.py:9-21) while its loads are in flight,
-// with the same arithmetic as the table kernels (rope_math.h), so both give identical bits.
+// lane computes the cos / sin of its 4 pairs (rope.py:9-21) while its loads are in flight.
+// The pair frequencies are computed once per block, into LDS.  Both use the table kernels'
+// arithmetic (rope_math.h), so the two sources give identical bits.
 //
 // The kernel is HBM-bound: per (b, t, h) it moves 3*256 bytes in and 3*256 out.
 
@@ -94,6 +95,18 @@ __global__ __launch_bounds__(kThreads) void qk_prep_kernel(
     uint16_t* __restrict__ v_out, int64_t out_length, int64_t out_offset) {
   const int lane = threadIdx.x & (kLanesPerRow - 1);
   const int t = blockIdx.x * kTokensPerBlock + (threadIdx.x >> 4);
+  // With ids, the block's first kHeadDim/2 threads compute each pair's frequency (and axis)
+  // once, with the table kernels' code, for every token of the block.
+  __shared__ float pair_freq[kIds ? kHeadDim / 2 : 1];
+  __shared__ int pair_axis[kIds ? kHeadDim / 2 : 1];
+  if constexpr (kIds) {
+    if (threadIdx.x < kHeadDim / 2) {
+      int axis;
+      pair_freq[threadIdx.x] = flk::pair_omega(threadIdx.x, rope.ax, rope.theta, axis);
+      pair_axis[threadIdx.x] = axis;
+    }
+    __syncthreads();
+  }
   if (t >= length) return;  // whole 16-lane rows exit together, so DPP rows stay intact
   const int h0 = blockIdx.y * kHeads;
   const int b = blockIdx.z;
@@ -113,10 +126,8 @@ __global__ __launch_bounds__(kThreads) void qk_prep_kernel(
     const float* pos = rope.ids + (int64_t)t * rope.ids_stride;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      int axis;
-      const float omega = flk::pair_omega(lane * 4 + j, rope.ax, rope.theta, axis);
       float cj, sj;
-      flk::pair_cos_sin(pos[axis], omega, cj, sj);
+      flk::pair_cos_sin(pos[pair_axis[lane * 4 + j]], pair_freq[lane * 4 + j], cj, sj);
       c[2 * j] = cj;
       c[2 * j + 1] = cj;
       s[2 * j] = -sj;
@@ -207,11 +218,11 @@ int dispatch(int hpg, int batch, int scale_is_f32, hipStream_t stream, const Lau
 
 // Heads per 16-lane group.  With tables, two measured best at the Klein shapes (6 loads in
 // flight per lane and 2x more blocks than four heads per group).  With ids, each group
-// computes 4 powf + 4 cos/sin pairs per token, so four heads (measured at 1024^2: 36.3 us
-// against 39.7 us for two, 36.9 us for six) share that work across 12 rows.
+// computes 4 cos/sin pairs per token, which more heads share: measured at 1024^2, six heads
+// 33.3 us, three 33.4, four 33.8, two 35.9.
 int heads_per_group(int num_heads, bool ids, int forced) {
   int hpg = (num_heads % 2 == 0) ? 2 : (num_heads % 3 == 0) ? 3 : 1;
-  if (ids && num_heads % 4 == 0) hpg = 4;
+  if (ids) hpg = (num_heads % 6 == 0) ? 6 : (num_heads % 4 == 0) ? 4 : (num_heads % 3 == 0) ? 3 : hpg;
   if (forced > 0 && num_heads % forced == 0) hpg = forced;
   return hpg;
 }
