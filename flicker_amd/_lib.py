@@ -7,6 +7,7 @@ first call raises ``HipLibraryMissing`` -- there is no CPU or PyTorch fallback.
 from __future__ import annotations
 
 import ctypes
+import functools
 import pathlib
 
 import torch
@@ -87,8 +88,9 @@ def check(status: int, what: str) -> None:
 
 
 def stream_of(t: torch.Tensor) -> int:
-    """Raw hipStream_t of torch's current stream on the tensor's device."""
-    return torch.cuda.current_stream(t.device).cuda_stream
+    """Raw hipStream_t of torch's current stream on the tensor's device (the integer handle,
+    without building a torch Stream object per call)."""
+    return torch._C._cuda_getCurrentRawStream(t.device.index)
 
 
 def device_of(*tensors) -> torch.device:
@@ -113,8 +115,10 @@ def ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
 
 
+@functools.lru_cache(maxsize=1024)
 def attend_plan(batch: int, heads: int, length: int) -> tuple[int, int]:
-    """(splits, workspace bytes) that flk_attend_plan picks for an attend of this shape."""
+    """(splits, workspace bytes) that flk_attend_plan picks for an attend of this shape (a
+    pure function of the shape, so cached)."""
     splits, nbytes = ctypes.c_int(0), ctypes.c_int64(0)
     check(lib().flk_attend_plan(batch, heads, length, ctypes.byref(splits), ctypes.byref(nbytes)),
           "flk_attend_plan")
