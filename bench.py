@@ -279,6 +279,33 @@ def w8a8_leg(args, timed, dev) -> dict:
 
     section(0)
     section_ms = timed(section, args.steps)
+    # A double block's two projections (modules.py:127-139): the first 512 tokens as the text
+    # stream with its own weight, the rest as the image stream, each modulated, into one joint
+    # q/k/v buffer -- two fused launches, or one for both (w8a8.qk_prep_pair).
+    double = None
+    if p.tokens > w_attn.num_txt:
+        from flicker_amd.kernels import Freqs
+        n_txt = w_attn.num_txt
+        _, w_cpu = workloads.make_projection(p)
+        qw_txt = w8a8.quantize_linear((-w_cpu).to(dev), w8a8.absmax_cols(x3[:, :n_txt]))
+        txt = (x3[:, :n_txt], qw_txt, qs, ks, Freqs(freqs.cos[:n_txt], freqs.sin[:n_txt], freqs.q_gain))
+        img = (x3[:, n_txt:], qw, qs, ks, Freqs(freqs.cos[n_txt:], freqs.sin[n_txt:], freqs.q_gain))
+
+        def two(i):
+            o = qkv_out[i % 2]
+            w8a8.qk_prep(*txt, heads, out=o, out_offset=0, modulation=(shift, scale))
+            w8a8.qk_prep(*img, heads, out=o, out_offset=n_txt, modulation=(shift, scale))
+
+        def pair(i):
+            w8a8.qk_prep_pair(txt, img, heads, out=qkv_out[i % 2], modulation=((shift, scale), (shift, scale)))
+
+        two(0)
+        pair(0)
+        double = {"text_tokens": n_txt, "image_tokens": p.tokens - n_txt,
+                  "two_launches_us": round(timed(two, args.steps) * 1e3, 2),
+                  "pair_us": round(timed(pair, args.steps) * 1e3, 2),
+                  "what": "modulate+quantise per stream, then the fused projection + qk_prep of both "
+                          "streams: two launches, or one (flk_w8a8_qk_prep_pair)"}
     del x3
     return {"workload": f"{p.name}: X ({p.tokens}, {p.hidden}) bf16 with {p.outlier_fraction:.0%} outlier "
                         f"channels x{p.outlier_gain:g}, W ({p.hidden}, {p.out_features}) ~ N(0, 0.02)",
@@ -291,6 +318,7 @@ def w8a8_leg(args, timed, dev) -> dict:
             "fused_gemm_qk_prep_us": round(fused_ms * 1e3, 2),
             "block_section_us": round(section_ms * 1e3, 2),
             "block_section": "modulate+quantise -> int8 projection with qk_prep epilogue -> attend_merged",
+            "double_block_projection": double,
             "dtype": "int8 operands, int32 accumulate, bf16 out"}
 
 

@@ -41,6 +41,9 @@ SIGNATURES = {
     "flk_w8a8_gemm": (_i, [_p, _p, _p, _p, _i, _i, _i, _p, _i64, _p, _p]),
     "flk_w8a8_qk_prep": (_i, [_p, _p, _p, _p, _i, _p, _p, _i64, _p, _p, _i, _f, _i, _i, _i, _i,
                               _p, _p, _p, _i64, _i64, _p]),
+    "flk_w8a8_qk_prep_pair": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _i, _i64,
+                                   _p, _p, _p, _p, _p, _p, _p, _p, _i, _i64,
+                                   _i, _i64, _i, _f, _i, _i, _i, _p, _p, _p, _i64, _p]),
 }
 
 ABI_VERSION = 1

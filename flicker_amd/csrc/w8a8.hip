@@ -33,6 +33,8 @@
 // share an XCD (and its L2), and grouped so that 4 token tiles sweep the channel tiles
 // together.
 
+#include <algorithm>
+
 #include "qk_math.h"
 
 namespace {
@@ -398,25 +400,55 @@ struct QkEpilogue {
   int64_t out_length, out_offset;
 };
 
+// One projection Y = X W^T of a launch (xq M x K, wqt N x K), with its outputs.
+struct GemmProblem {
+  const int8_t* xq;
+  const int8_t* wqt;
+  const float* a_scale;
+  const float* w_scale;
+  uint16_t* y;            // plain epilogue: Y rows of y_stride elements
+  int64_t y_stride;
+  int32_t* acc_out;       // kAcc: the exact int32 products
+  int M, K, N, tiles_m, tiles_n;
+  QkEpilogue qe;          // kQk: qk_prep epilogue
+};
+
+// Up to two projections in one launch, so that a small one (a double block's 512 text
+// tokens: 72 tiles) fills the CUs the large one (the image tokens) leaves idle in its last
+// round.  Logical blocks [0, first_blocks) take p[0], the rest p[1].
+struct GemmGroup {
+  GemmProblem p[2];
+  int first_blocks;
+};
+
 // kAcc: also write the exact int32 products (a test and debugging path).
 // kQk: instead of Y, run qk_prep on each finished bf16 head row (kScaleF32: float32 norm
 // scales) and write head-major q, k, v.
 template <bool kAcc, bool kQk = false, bool kScaleF32 = false>
-__global__ __launch_bounds__(kGThreads, 2) void w8a8_gemm_kernel(
-    const int8_t* __restrict__ xq, const int8_t* __restrict__ wqt, const float* __restrict__ a_scale,
-    const float* __restrict__ w_scale, uint16_t* __restrict__ y, int64_t y_stride,
-    int32_t* __restrict__ acc_out, int M, int K, int N, int tiles_m, int tiles_n, QkEpilogue qe) {
+__global__ __launch_bounds__(kGThreads, 2) void w8a8_gemm_kernel(const GemmGroup grp) {
   __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * kGStage];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 
   // Tile order: blocks are dealt round-robin over the XCDs; renumber so that each XCD runs
-  // a contiguous range of logical tiles, then walk kGroup token tiles across all channel
-  // tiles before moving on.
+  // a contiguous range of logical tiles (of one problem, then the next), then walk kGroup
+  // token tiles across all channel tiles before moving on.
   const int nblocks = gridDim.x;
   const int xcd = blockIdx.x % kXcds, local = blockIdx.x / kXcds;
   const int per = nblocks / kXcds, extra = nblocks % kXcds;
-  const int logical = xcd * per + min(xcd, extra) + local;
+  const int logical_all = xcd * per + min(xcd, extra) + local;
+  const bool second = logical_all >= grp.first_blocks;
+  const GemmProblem& P = second ? grp.p[1] : grp.p[0];   // wave-uniform, read from the kernel arguments
+  const int logical = logical_all - (second ? grp.first_blocks : 0);
+  const int8_t* __restrict__ xq = P.xq;
+  const int8_t* __restrict__ wqt = P.wqt;
+  const float* __restrict__ a_scale = P.a_scale;
+  const float* __restrict__ w_scale = P.w_scale;
+  uint16_t* __restrict__ y = P.y;
+  const int64_t y_stride = P.y_stride;
+  int32_t* __restrict__ acc_out = P.acc_out;
+  const int M = P.M, K = P.K, N = P.N, tiles_m = P.tiles_m, tiles_n = P.tiles_n;
+  const QkEpilogue& qe = P.qe;
   const int group_tiles = kGroup * tiles_n;
   const int group = logical / group_tiles;
   const int first_m = group * kGroup;
@@ -723,41 +755,30 @@ extern "C" int flk_quantize_act_modulated(const void* x, int64_t x_row_stride, c
   return flk_launch_status();
 }
 
-extern "C" int flk_w8a8_gemm(const int8_t* xq, const int8_t* wq_t, const float* a_scale, const float* w_scale,
-                             int m, int k, int n, void* y, int64_t y_row_stride, int32_t* acc_or_null,
-                             void* stream) {
-  if (m < 0 || k < 0 || n < 0 || y_row_stride < n) return FLK_E_INVALID;
-  if (m == 0 || n == 0) return FLK_OK;
-  if (!xq || !wq_t || !a_scale || !w_scale || !y || k == 0) return FLK_E_INVALID;
-  if (k % 128 || n % 4) return FLK_E_UNSUPPORTED;
-  if ((int64_t)k * 127 * 127 > INT32_MAX) return FLK_E_UNSUPPORTED;   // int32 accumulation must be exact
-  if (!flk_host_aligned(xq, 16) || !flk_host_aligned(wq_t, 16) || !flk_host_aligned(w_scale, 16) ||
-      !flk_host_aligned(a_scale, 4) || !flk_host_aligned(y, 8) || y_row_stride % 4 ||
-      (acc_or_null && !flk_host_aligned(acc_or_null, 16)))
-    return FLK_E_ALIGN;
-  const int tiles_m = (m + kGT - 1) / kGT, tiles_n = (n + kGT - 1) / kGT;
-  const int64_t blocks = (int64_t)tiles_m * tiles_n;
+namespace {
+
+int64_t problem_blocks(const GemmProblem& p) { return (int64_t)p.tiles_m * p.tiles_n; }
+
+template <bool kAcc, bool kQk, bool kScaleF32>
+int launch_group(const GemmGroup& g, int64_t blocks, void* stream) {
   if (blocks > INT32_MAX) return FLK_E_INVALID;
-  if (acc_or_null)
-    hipLaunchKernelGGL(w8a8_gemm_kernel<true>, dim3((unsigned)blocks), dim3(kGThreads), 0, as_stream(stream), xq,
-                       wq_t, a_scale, w_scale, static_cast<uint16_t*>(y), y_row_stride, acc_or_null, m, k, n, tiles_m,
-                       tiles_n, QkEpilogue{});
-  else
-    hipLaunchKernelGGL(w8a8_gemm_kernel<false>, dim3((unsigned)blocks), dim3(kGThreads), 0, as_stream(stream), xq,
-                       wq_t, a_scale, w_scale, static_cast<uint16_t*>(y), y_row_stride, nullptr, m, k, n, tiles_m,
-                       tiles_n, QkEpilogue{});
+  hipLaunchKernelGGL((w8a8_gemm_kernel<kAcc, kQk, kScaleF32>), dim3((unsigned)blocks), dim3(kGThreads), 0,
+                     as_stream(stream), g);
   return flk_launch_status();
 }
 
-extern "C" int flk_w8a8_qk_prep(const int8_t* xq, const int8_t* wq_t, const float* a_scale, const float* w_scale,
-                                int k, const float* cos, const float* sin, int64_t table_row_stride,
-                                const void* q_scale, const void* k_scale, int scale_is_f32, float q_gain, int batch,
-                                int length, int num_heads, int head_dim, void* q_out, void* k_out, void* v_out,
-                                int64_t out_length, int64_t out_offset, void* stream) {
+// Checks one fused projection + qk_prep (flk_w8a8_qk_prep's arguments) and fills its
+// problem.  FLK_OK = launch, kNoWork = empty (nothing to launch), else an error status.
+constexpr int kNoWork = 1;
+
+int qk_problem(const int8_t* xq, const int8_t* wq_t, const float* a_scale, const float* w_scale, int k,
+               const float* cos, const float* sin, int64_t table_row_stride, const void* q_scale,
+               const void* k_scale, float q_gain, int batch, int length, int num_heads, int head_dim,
+               void* q_out, void* k_out, void* v_out, int64_t out_length, int64_t out_offset, GemmProblem& p) {
   if (head_dim != flk::kQkHeadDim) return FLK_E_UNSUPPORTED;
   if (batch < 0 || length < 0 || num_heads <= 0 || k < 0 || out_offset < 0 || out_offset + length > out_length)
     return FLK_E_INVALID;
-  if (batch == 0 || length == 0) return FLK_OK;
+  if (batch == 0 || length == 0) return kNoWork;
   if (!xq || !wq_t || !a_scale || !w_scale || !cos || !sin || !q_scale || !k_scale || !q_out || !k_out ||
       !v_out || k == 0 || table_row_stride < head_dim)
     return FLK_E_INVALID;
@@ -770,20 +791,100 @@ extern "C" int flk_w8a8_qk_prep(const int8_t* xq, const int8_t* wq_t, const floa
       table_row_stride % 4 || !flk_host_aligned(q_scale, 16) || !flk_host_aligned(k_scale, 16) ||
       !flk_host_aligned(q_out, 16) || !flk_host_aligned(k_out, 16) || !flk_host_aligned(v_out, 16))
     return FLK_E_ALIGN;
-  const int m = (int)m64;
-  const int tiles_m = (m + kGT - 1) / kGT, tiles_n = (int)((n + kGT - 1) / kGT);
-  const int64_t blocks = (int64_t)tiles_m * tiles_n;
-  if (blocks > INT32_MAX) return FLK_E_INVALID;
-  QkEpilogue qe{cos, sin, table_row_stride, q_scale, k_scale, q_gain, length, num_heads,
-                {static_cast<uint16_t*>(q_out), static_cast<uint16_t*>(k_out), static_cast<uint16_t*>(v_out)},
-                out_length, out_offset};
-  if (scale_is_f32)
-    hipLaunchKernelGGL((w8a8_gemm_kernel<false, true, true>), dim3((unsigned)blocks), dim3(kGThreads), 0,
-                       as_stream(stream), xq, wq_t, a_scale, w_scale, nullptr, 0, nullptr, m, k, (int)n, tiles_m,
-                       tiles_n, qe);
-  else
-    hipLaunchKernelGGL((w8a8_gemm_kernel<false, true, false>), dim3((unsigned)blocks), dim3(kGThreads), 0,
-                       as_stream(stream), xq, wq_t, a_scale, w_scale, nullptr, 0, nullptr, m, k, (int)n, tiles_m,
-                       tiles_n, qe);
-  return flk_launch_status();
+  p = GemmProblem{};
+  p.xq = xq;
+  p.wqt = wq_t;
+  p.a_scale = a_scale;
+  p.w_scale = w_scale;
+  p.M = (int)m64;
+  p.K = k;
+  p.N = (int)n;
+  p.tiles_m = (p.M + kGT - 1) / kGT;
+  p.tiles_n = (p.N + kGT - 1) / kGT;
+  p.qe = QkEpilogue{cos, sin, table_row_stride, q_scale, k_scale, q_gain, length, num_heads,
+                    {static_cast<uint16_t*>(q_out), static_cast<uint16_t*>(k_out), static_cast<uint16_t*>(v_out)},
+                    out_length, out_offset};
+  return FLK_OK;
+}
+
+int launch_qk(const GemmGroup& g, int64_t blocks, int scale_is_f32, void* stream) {
+  return scale_is_f32 ? launch_group<false, true, true>(g, blocks, stream)
+                      : launch_group<false, true, false>(g, blocks, stream);
+}
+
+}  // namespace
+
+extern "C" int flk_w8a8_gemm(const int8_t* xq, const int8_t* wq_t, const float* a_scale, const float* w_scale,
+                             int m, int k, int n, void* y, int64_t y_row_stride, int32_t* acc_or_null,
+                             void* stream) {
+  if (m < 0 || k < 0 || n < 0 || y_row_stride < n) return FLK_E_INVALID;
+  if (m == 0 || n == 0) return FLK_OK;
+  if (!xq || !wq_t || !a_scale || !w_scale || !y || k == 0) return FLK_E_INVALID;
+  if (k % 128 || n % 4) return FLK_E_UNSUPPORTED;
+  if ((int64_t)k * 127 * 127 > INT32_MAX) return FLK_E_UNSUPPORTED;   // int32 accumulation must be exact
+  if (!flk_host_aligned(xq, 16) || !flk_host_aligned(wq_t, 16) || !flk_host_aligned(w_scale, 16) ||
+      !flk_host_aligned(a_scale, 4) || !flk_host_aligned(y, 8) || y_row_stride % 4 ||
+      (acc_or_null && !flk_host_aligned(acc_or_null, 16)))
+    return FLK_E_ALIGN;
+  GemmGroup g{};
+  GemmProblem& p = g.p[0];
+  p.xq = xq;
+  p.wqt = wq_t;
+  p.a_scale = a_scale;
+  p.w_scale = w_scale;
+  p.y = static_cast<uint16_t*>(y);
+  p.y_stride = y_row_stride;
+  p.acc_out = acc_or_null;
+  p.M = m;
+  p.K = k;
+  p.N = n;
+  p.tiles_m = (m + kGT - 1) / kGT;
+  p.tiles_n = (n + kGT - 1) / kGT;
+  g.p[1] = p;
+  const int64_t blocks = problem_blocks(p);
+  g.first_blocks = (int)std::min<int64_t>(blocks, INT32_MAX);
+  return acc_or_null ? launch_group<true, false, false>(g, blocks, stream)
+                     : launch_group<false, false, false>(g, blocks, stream);
+}
+
+extern "C" int flk_w8a8_qk_prep(const int8_t* xq, const int8_t* wq_t, const float* a_scale, const float* w_scale,
+                                int k, const float* cos, const float* sin, int64_t table_row_stride,
+                                const void* q_scale, const void* k_scale, int scale_is_f32, float q_gain, int batch,
+                                int length, int num_heads, int head_dim, void* q_out, void* k_out, void* v_out,
+                                int64_t out_length, int64_t out_offset, void* stream) {
+  GemmGroup g{};
+  const int st = qk_problem(xq, wq_t, a_scale, w_scale, k, cos, sin, table_row_stride, q_scale, k_scale, q_gain,
+                            batch, length, num_heads, head_dim, q_out, k_out, v_out, out_length, out_offset, g.p[0]);
+  if (st != FLK_OK) return st == kNoWork ? FLK_OK : st;
+  g.p[1] = g.p[0];
+  const int64_t blocks = problem_blocks(g.p[0]);
+  g.first_blocks = (int)std::min<int64_t>(blocks, INT32_MAX);
+  return launch_qk(g, blocks, scale_is_f32, stream);
+}
+
+extern "C" int flk_w8a8_qk_prep_pair(
+    const int8_t* xq0, const int8_t* wq_t0, const float* a_scale0, const float* w_scale0, const float* cos0,
+    const float* sin0, const void* q_scale0, const void* k_scale0, int length0, int64_t out_offset0,
+    const int8_t* xq1, const int8_t* wq_t1, const float* a_scale1, const float* w_scale1, const float* cos1,
+    const float* sin1, const void* q_scale1, const void* k_scale1, int length1, int64_t out_offset1, int k,
+    int64_t table_row_stride, int scale_is_f32, float q_gain, int batch, int num_heads, int head_dim, void* q_out,
+    void* k_out, void* v_out, int64_t out_length, void* stream) {
+  GemmGroup g{};
+  const int st0 = qk_problem(xq0, wq_t0, a_scale0, w_scale0, k, cos0, sin0, table_row_stride, q_scale0, k_scale0,
+                             q_gain, batch, length0, num_heads, head_dim, q_out, k_out, v_out, out_length,
+                             out_offset0, g.p[0]);
+  if (st0 != FLK_OK && st0 != kNoWork) return st0;
+  const int st1 = qk_problem(xq1, wq_t1, a_scale1, w_scale1, k, cos1, sin1, table_row_stride, q_scale1, k_scale1,
+                             q_gain, batch, length1, num_heads, head_dim, q_out, k_out, v_out, out_length,
+                             out_offset1, g.p[1]);
+  if (st1 != FLK_OK && st1 != kNoWork) return st1;
+  if (st0 == kNoWork && st1 == kNoWork) return FLK_OK;
+  // An empty problem gives its place to the other one, which then takes every block.
+  if (st0 == kNoWork) g.p[0] = g.p[1];
+  if (st1 == kNoWork) g.p[1] = g.p[0];
+  const bool both = st0 == FLK_OK && st1 == FLK_OK;
+  const int64_t b0 = problem_blocks(g.p[0]);
+  const int64_t blocks = both ? b0 + problem_blocks(g.p[1]) : b0;
+  g.first_blocks = (int)std::min<int64_t>(b0, INT32_MAX);
+  return launch_qk(g, blocks, scale_is_f32, stream);
 }

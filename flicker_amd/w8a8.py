@@ -203,18 +203,9 @@ def linear(x: torch.Tensor, qw: QuantizedLinear, *, out: torch.Tensor | None = N
     return y.reshape(*lead, qw.out_features) if out is None else out
 
 
-def qk_prep(x: torch.Tensor, qw: QuantizedLinear, q_scale: torch.Tensor, k_scale: torch.Tensor, freqs,
-            num_heads: int, *, out=None, out_offset: int = 0, modulation=None):
-    """``kernels.qk_prep(linear(x, qw), q_scale, k_scale, freqs, num_heads)`` in two launches
-    instead of three: the activation quantisation, then one int8 GEMM whose epilogue applies
-    QK-RMSNorm + RoPE (+ q_gain) to each finished head row and writes head-major q, k, v
-    (kernels.py:57-91 after nn.py:13-14); the projected activation never reaches memory.
-    Bit-identical to the unfused pair.  x (B, L, K) bf16 -> q, k, v (B, H, L, 128) bf16.
-
-    With ``modulation=(shift, scale)`` x is the raw block input and the projection input is
-    modulate(x, shift, scale) (modules.py:38-40), computed inside the activation quantisation:
-    the whole ``qkv_prep(linear(modulate(x, mod1), w), ...)`` of a block (modules.py:128-133,
-    186-190) is then two launches."""
+def _qk_stream(x, qw: QuantizedLinear, q_scale, k_scale, freqs, num_heads: int, modulation):
+    """Checks and device operands of one fused projection + qk_prep stream: (xq, a_scale, cos,
+    sin, q_scale, k_scale, q_gain), the activation quantised (modulated first when given)."""
     from .kernels import HEAD_DIM, Freqs, PositionIds
 
     if x.dim() != 3:
@@ -224,7 +215,7 @@ def qk_prep(x: torch.Tensor, qw: QuantizedLinear, q_scale: torch.Tensor, k_scale
         # arithmetic the in-kernel form uses, so the values are identical.
         from .rope import rope_lanes
         freqs = rope_lanes(freqs.ids, freqs.q_gain, freqs.axes_dim, freqs.theta)
-    batch, length, k = x.shape
+    length = x.shape[1]
     if qw.out_features != 3 * num_heads * HEAD_DIM:
         raise ValueError(f"projection has {qw.out_features} outputs, not 3 * {num_heads} * {HEAD_DIM}")
     cos, sin, q_gain = Freqs(*freqs)
@@ -242,6 +233,26 @@ def qk_prep(x: torch.Tensor, qw: QuantizedLinear, q_scale: torch.Tensor, k_scale
         xq, a_scale = quantize_act(x, qw.inv_smooth)
     else:
         xq, a_scale = quantize_act_modulated(x, modulation[0], modulation[1], qw.inv_smooth)
+    return xq, a_scale, cos, sin, q_scale, k_scale, float(q_gain)
+
+
+def qk_prep(x: torch.Tensor, qw: QuantizedLinear, q_scale: torch.Tensor, k_scale: torch.Tensor, freqs,
+            num_heads: int, *, out=None, out_offset: int = 0, modulation=None):
+    """``kernels.qk_prep(linear(x, qw), q_scale, k_scale, freqs, num_heads)`` in two launches
+    instead of three: the activation quantisation, then one int8 GEMM whose epilogue applies
+    QK-RMSNorm + RoPE (+ q_gain) to each finished head row and writes head-major q, k, v
+    (kernels.py:57-91 after nn.py:13-14); the projected activation never reaches memory.
+    Bit-identical to the unfused pair.  x (B, L, K) bf16 -> q, k, v (B, H, L, 128) bf16.
+
+    With ``modulation=(shift, scale)`` x is the raw block input and the projection input is
+    modulate(x, shift, scale) (modules.py:38-40), computed inside the activation quantisation:
+    the whole ``qkv_prep(linear(modulate(x, mod1), w), ...)`` of a block (modules.py:128-133,
+    186-190) is then two launches."""
+    from .kernels import HEAD_DIM
+
+    s = _qk_stream(x, qw, q_scale, k_scale, freqs, num_heads, modulation)
+    batch, length, k = x.shape
+    xq, a_scale, cos, sin, q_scale, k_scale, q_gain = s
     if out is None:
         if out_offset:
             raise ValueError("out_offset needs out=(q, k, v)")
@@ -262,4 +273,56 @@ def qk_prep(x: torch.Tensor, qw: QuantizedLinear, q_scale: torch.Tensor, k_scale
              sin.data_ptr(), cos.stride(0), q_scale.data_ptr(), k_scale.data_ptr(),
              int(q_scale.dtype == torch.float32), float(q_gain), batch, length, num_heads, HEAD_DIM,
              out[0].data_ptr(), out[1].data_ptr(), out[2].data_ptr(), out_length, out_offset, _lib.stream_of(x))
+    return out
+
+
+def qk_prep_pair(txt, img, num_heads: int, *, out=None, modulation=None):
+    """A double block's two projections with their qk prep (modules.py:127-135: txt_attn.qkv
+    and img_attn.qkv, each followed by qkv_prep) plus the text|image concatenations
+    (modules.py:136-139), in one fused launch after one activation quantisation per stream.
+    The text projection's 512 tokens run on the CUs the image projection leaves idle in its
+    last round.
+
+    ``txt`` and ``img`` are (x, qw, q_scale, k_scale, freqs): each stream's (B, L_i, K) input,
+    quantised weight, norm scales and RoPE lanes of its own rows.  ``modulation`` is
+    optionally ((shift_txt, scale_txt), (shift_img, scale_img)).  Returns the joint q, k, v
+    (B, H, L_txt + L_img, 128), text first (or writes ``out``); each stream's rows are
+    bit-identical to ``qk_prep`` of that stream alone."""
+    from .kernels import HEAD_DIM
+
+    mods = modulation if modulation is not None else (None, None)
+    s0 = _qk_stream(*txt, num_heads, mods[0])
+    s1 = _qk_stream(*img, num_heads, mods[1])
+    x0, x1 = txt[0], img[0]
+    if x0.shape[0] != x1.shape[0] or x0.shape[2] != x1.shape[2]:
+        raise ValueError(f"text and image inputs must share batch and width, got {tuple(x0.shape)} "
+                         f"and {tuple(x1.shape)}")
+    if s0[6] != s1[6]:
+        raise ValueError(f"both streams must share q_gain, got {s0[6]} and {s1[6]}")
+    if s0[4].dtype != s1[4].dtype:
+        raise ValueError("both streams' norm scales must share one dtype")
+    batch, len0, k = x0.shape
+    len1 = x1.shape[1]
+    if out is None:
+        out = tuple(torch.empty((batch, num_heads, len0 + len1, HEAD_DIM), dtype=torch.bfloat16,
+                                device=x0.device) for _ in range(3))
+    else:
+        out = tuple(out)
+        for t in out:
+            if (t.dtype != torch.bfloat16 or t.shape != (batch, num_heads, len0 + len1, HEAD_DIM)
+                    or not t.is_contiguous()):
+                raise ValueError(f"out tensors must be contiguous bf16 ({batch}, {num_heads}, "
+                                 f"{len0 + len1}, {HEAD_DIM})")
+
+    def stream_args(st, qw, length, offset):
+        xq, a_scale, cos, sin, q_scale, k_scale, _ = st
+        return (xq.data_ptr(), qw.wq_t.data_ptr(), a_scale.data_ptr(), qw.w_scale.data_ptr(), cos.data_ptr(),
+                sin.data_ptr(), q_scale.data_ptr(), k_scale.data_ptr(), length, offset)
+
+    operands = (s0[0], txt[1].wq_t, s0[1], txt[1].w_scale, *s0[2:6],
+                s1[0], img[1].wq_t, s1[1], img[1].w_scale, *s1[2:6], *out)
+    _lib.run("flk_w8a8_qk_prep_pair", operands,
+             *stream_args(s0, txt[1], len0, 0), *stream_args(s1, img[1], len1, len0),
+             k, HEAD_DIM, int(s0[4].dtype == torch.float32), s0[6], batch, num_heads, HEAD_DIM,
+             out[0].data_ptr(), out[1].data_ptr(), out[2].data_ptr(), len0 + len1, _lib.stream_of(x0))
     return out

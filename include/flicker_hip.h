@@ -224,6 +224,30 @@ int flk_w8a8_qk_prep(const int8_t* xq, const int8_t* wq_t, const float* a_scale,
                      void* q_out, void* k_out, void* v_out, int64_t out_length, int64_t out_offset,
                      void* stream);
 
+/* Two flk_w8a8_qk_prep projections in one launch, writing into the same q/k/v buffers:
+ * a double block's text and image streams.  Replaces the two linear + qk_prep pairs of
+ * modules.py:127-135 (txt_attn.qkv and img_attn.qkv, each with its own norm scales and RoPE
+ * rows) followed by the concatenations of modules.py:136-139.  The small text projection
+ * (512 tokens, 72 tiles) runs on the CUs the image projection leaves idle in its last
+ * round, instead of taking a launch of its own.
+ *
+ * Per stream i: xq_i (batch*length_i, k), wq_t_i, a_scale_i, w_scale_i, cos_i/sin_i (length_i
+ * rows), q_scale_i/k_scale_i, and the sequence offset out_offset_i at which its tokens go.
+ * Shared: k, table_row_stride, scale_is_f32, q_gain, batch, num_heads, head_dim, the
+ * outputs and out_length.
+ *
+ * Each stream gets exactly flk_w8a8_qk_prep's result (bit-identical); an empty stream
+ * (length_i == 0) is skipped. */
+int flk_w8a8_qk_prep_pair(const int8_t* xq0, const int8_t* wq_t0, const float* a_scale0, const float* w_scale0,
+                          const float* cos0, const float* sin0, const void* q_scale0, const void* k_scale0,
+                          int length0, int64_t out_offset0,
+                          const int8_t* xq1, const int8_t* wq_t1, const float* a_scale1, const float* w_scale1,
+                          const float* cos1, const float* sin1, const void* q_scale1, const void* k_scale1,
+                          int length1, int64_t out_offset1,
+                          int k, int64_t table_row_stride, int scale_is_f32, float q_gain, int batch,
+                          int num_heads, int head_dim, void* q_out, void* k_out, void* v_out,
+                          int64_t out_length, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -325,6 +325,36 @@ def test_modulated_projection_qk_prep(device):
         assert torch.equal(a.view(torch.int16), b.view(torch.int16))
 
 
+@pytest.mark.parametrize("batch,len0,len1,heads,k,scale_dtype,modulated", [
+    (1, 512, 4096, 24, 3072, torch.bfloat16, False),   # a Klein double block: 512 text + 64x64 image tokens
+    (2, 70, 300, 2, 256, torch.float32, True),          # ragged streams, f32 scales, modulated inputs
+    (1, 0, 130, 2, 128, torch.bfloat16, False),         # an empty text stream
+])
+def test_fused_projection_pair_equals_two_calls(device, batch, len0, len1, heads, k, scale_dtype, modulated):
+    """flk_w8a8_qk_prep_pair (both streams of a double block in one launch) writes exactly what
+    two flk_w8a8_qk_prep calls write at sequence offsets 0 and L_txt: each stream has its own
+    weights, norm scales, RoPE rows and (optionally) modulation."""
+    from flicker_amd.kernels import Freqs
+    gain = 128 ** -0.5
+    streams, mods = [], []
+    for i, n in enumerate((len0, len1)):
+        x, qw, qs, ks, freqs, _ = _fused_case(device, batch, max(n, 1), heads, k, scale_dtype, gain, seed=40 + i)
+        streams.append((x[:, :n].contiguous(), qw, qs, ks, Freqs(freqs.cos[:n], freqs.sin[:n], freqs.q_gain)))
+        g = torch.Generator().manual_seed(50 + i)
+        mods.append(((0.3 * torch.randn(batch, k, generator=g)).to(torch.bfloat16).to(device),
+                     (0.1 * torch.randn(batch, k, generator=g)).to(torch.bfloat16).to(device)))
+    mods = mods if modulated else [None, None]
+    want = tuple(torch.full((batch, heads, len0 + len1, 128), 5.0, dtype=torch.bfloat16, device=device)
+                 for _ in range(3))
+    w8a8.qk_prep(*streams[0], heads, out=want, out_offset=0, modulation=mods[0])
+    w8a8.qk_prep(*streams[1], heads, out=want, out_offset=len0, modulation=mods[1])
+    got = w8a8.qk_prep_pair(streams[0], streams[1], heads, modulation=(mods[0], mods[1]) if modulated else None)
+    torch.cuda.synchronize()
+    for name, a, b in zip("qkv", got, want):
+        bad = int((a.view(torch.int16) != b.view(torch.int16)).sum())
+        assert bad == 0, f"{name}: {bad} of {a.numel()} elements differ"
+
+
 def test_errors(device):
     x = torch.zeros((4, 100), dtype=torch.bfloat16, device=device)
     with pytest.raises(Exception, match="status -3"):        # k % 8
