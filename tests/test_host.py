@@ -270,6 +270,17 @@ def test_w8a8_validation(lib):
     assert lib.flk_absmax_rows(FAKE, 4, 12, 12, FAKE, None) == _lib.FLK_E_ALIGN
     assert lib.flk_absmax_cols(FAKE, 4, 16, 8, 0, FAKE, None) == _lib.FLK_E_INVALID
     assert lib.flk_smooth_factors(FAKE, FAKE, -1, FAKE, FAKE, None) == _lib.FLK_E_INVALID
+    pair = lib.flk_w8a8_qk_prep_pair
+
+    def stream(length, offset, ptr=FAKE):
+        return (ptr, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, length, offset)
+
+    tail = (3072, 128, 0, 1.0, 1, 24, 128, FAKE, FAKE, FAKE, 4608, None)
+    assert pair(*stream(512, 0), *stream(4096, 512), *tail[:6], 64, *tail[7:]) == _lib.FLK_E_UNSUPPORTED
+    assert pair(*stream(-1, 0), *stream(4096, 512), *tail) == _lib.FLK_E_INVALID
+    assert pair(*stream(512, 0), *stream(4096, 600), *tail) == _lib.FLK_E_INVALID     # past out_length
+    assert pair(*stream(512, 0, FAKE + 4), *stream(4096, 512), *tail) == _lib.FLK_E_ALIGN
+    assert pair(*stream(0, 0), *stream(0, 0), *tail) == _lib.FLK_OK                  # both empty
 
 
 def test_w8a8_python_errors():
