@@ -38,6 +38,8 @@ SIGNATURES = {
     "flk_quantize_weight": (_i, [_p, _i64, _p, _i, _i, _p, _p, _p]),
     "flk_quantize_act": (_i, [_p, _i64, _p, _i, _i, _p, _p, _p]),
     "flk_quantize_act_modulated": (_i, [_p, _i64, _p, _p, _i64, _i, _p, _i, _i, _p, _p, _p, _i64, _p]),
+    "flk_quantize_act_modulated_pair": (_i, [_p, _i64, _p, _p, _i64, _i, _p, _i, _p, _p, _p, _i64,
+                                             _p, _i64, _p, _p, _i64, _i, _p, _i, _p, _p, _p, _i64, _i, _p]),
     "flk_w8a8_gemm": (_i, [_p, _p, _p, _p, _i, _i, _i, _p, _i64, _p, _p]),
     "flk_w8a8_qk_prep": (_i, [_p, _p, _p, _p, _i, _p, _p, _i64, _p, _p, _i, _f, _i, _i, _i, _i,
                               _p, _p, _p, _i64, _i64, _p]),

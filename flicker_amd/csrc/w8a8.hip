@@ -232,17 +232,48 @@ __device__ __forceinline__ double wave_sum(double v) {
   return v;
 }
 
+// One activation of a quantisation launch (rows of M tokens, all of width K).
+struct QuantProblem {
+  const uint16_t* x;
+  int64_t x_stride;
+  const float* inv_s;
+  int M;
+  int8_t* xq;
+  float* a_scale;
+  const uint16_t* shift;    // kModulate: modulation rows of each batch entry
+  const uint16_t* scale;
+  int64_t mod_stride;
+  int tokens_per_batch;
+  uint16_t* x_mod;          // kModulate: optional store of the modulated input
+  int64_t x_mod_stride;
+};
+
+// Up to two activations in one launch (a double block's text and image streams): blocks
+// [0, first_blocks) take p[0], the rest p[1]; four rows per block.
+struct QuantGroup {
+  QuantProblem p[2];
+  int first_blocks;
+  int K;
+};
+
 template <int kChunks, bool kModulate>
-__global__ __launch_bounds__(256) void quantize_act_kernel(const uint16_t* __restrict__ x, int64_t x_stride,
-                                                           const float* __restrict__ inv_s, int M, int K,
-                                                           int8_t* __restrict__ xq,
-                                                           float* __restrict__ a_scale,
-                                                           const uint16_t* __restrict__ shift,
-                                                           const uint16_t* __restrict__ scale,
-                                                           int64_t mod_stride, int tokens_per_batch,
-                                                           uint16_t* __restrict__ x_mod, int64_t x_mod_stride) {
+__global__ __launch_bounds__(256) void quantize_act_kernel(const QuantGroup grp) {
+  const bool second = (int)blockIdx.x >= grp.first_blocks;
+  const QuantProblem& P = second ? grp.p[1] : grp.p[0];   // wave-uniform, read from the kernel arguments
+  const uint16_t* __restrict__ x = P.x;
+  const int64_t x_stride = P.x_stride;
+  const float* __restrict__ inv_s = P.inv_s;
+  const int M = P.M, K = grp.K;
+  int8_t* __restrict__ xq = P.xq;
+  float* __restrict__ a_scale = P.a_scale;
+  const uint16_t* __restrict__ shift = P.shift;
+  const uint16_t* __restrict__ scale = P.scale;
+  const int64_t mod_stride = P.mod_stride;
+  const int tokens_per_batch = P.tokens_per_batch;
+  uint16_t* __restrict__ x_mod = P.x_mod;
+  const int64_t x_mod_stride = P.x_mod_stride;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int row = blockIdx.x * 4 + wave;
+  const int row = ((int)blockIdx.x - (second ? grp.first_blocks : 0)) * 4 + wave;
   if (row >= M) return;
   const int nch = K >> 3;
   const uint16_t* src = x + (int64_t)row * x_stride;
@@ -700,12 +731,12 @@ extern "C" int flk_quantize_weight(const void* w, int64_t w_row_stride, const fl
 namespace {
 
 template <bool kModulate>
-void launch_quantize_act(int chunks, dim3 grid, hipStream_t st, const uint16_t* xs, int64_t xstride,
-                         const float* inv_s, int m, int k, int8_t* xq, float* a_scale, const uint16_t* shift,
-                         const uint16_t* scale, int64_t mod_stride, int tokens, uint16_t* x_mod, int64_t xm_stride) {
-  const dim3 block(256);
-#define FLK_QA(C) hipLaunchKernelGGL((quantize_act_kernel<C, kModulate>), grid, block, 0, st, xs, xstride, inv_s, m, k, \
-                                     xq, a_scale, shift, scale, mod_stride, tokens, x_mod, xm_stride)
+int launch_quantize_act(const QuantGroup& g, int64_t blocks, void* stream) {
+  if (blocks > INT32_MAX) return FLK_E_INVALID;
+  const int chunks = (g.K / 8 + 63) / 64;
+  const dim3 grid((unsigned)blocks), block(256);
+  const hipStream_t st = as_stream(stream);
+#define FLK_QA(C) hipLaunchKernelGGL((quantize_act_kernel<C, kModulate>), grid, block, 0, st, g)
   if (chunks <= 1) FLK_QA(1);
   else if (chunks <= 2) FLK_QA(2);
   else if (chunks <= 4) FLK_QA(4);
@@ -714,7 +745,35 @@ void launch_quantize_act(int chunks, dim3 grid, hipStream_t st, const uint16_t* 
   else if (chunks <= 12) FLK_QA(12);
   else FLK_QA(16);
 #undef FLK_QA
+  return flk_launch_status();
 }
+
+// Status of a checked problem with nothing to launch (empty input).
+constexpr int kNoWork = 1;
+
+// Checks one modulated activation (flk_quantize_act_modulated's arguments) and fills its
+// problem: FLK_OK, kNoWork, or an error status.
+int modulated_problem(const void* x, int64_t x_row_stride, const void* shift, const void* scale,
+                      int64_t mod_batch_stride, int tokens_per_batch, const float* inv_s, int m, int k, int8_t* xq,
+                      float* a_scale, void* x_mod, int64_t x_mod_row_stride, QuantProblem& p) {
+  if (m < 0 || k < 0 || x_row_stride < k || mod_batch_stride < 0 || (x_mod && x_mod_row_stride < k))
+    return FLK_E_INVALID;
+  if (m == 0 || k == 0) return kNoWork;   // an empty input (its sequence length may be 0 too)
+  if (tokens_per_batch <= 0) return FLK_E_INVALID;
+  if (!x || !shift || !scale || !inv_s || !xq || !a_scale) return FLK_E_INVALID;
+  if ((m - 1) / tokens_per_batch > 0 && mod_batch_stride < k) return FLK_E_INVALID;
+  if (k % 8 || k > 8192) return FLK_E_UNSUPPORTED;
+  if (x_row_stride % 8 || mod_batch_stride % 8 || !flk_host_aligned(x, 16) || !flk_host_aligned(shift, 16) ||
+      !flk_host_aligned(scale, 16) || !flk_host_aligned(inv_s, 16) || !flk_host_aligned(xq, 8) ||
+      !flk_host_aligned(a_scale, 4) || (x_mod && (!flk_host_aligned(x_mod, 16) || x_mod_row_stride % 8)))
+    return FLK_E_ALIGN;
+  p = QuantProblem{static_cast<const uint16_t*>(x), x_row_stride, inv_s, m, xq, a_scale,
+                   static_cast<const uint16_t*>(shift), static_cast<const uint16_t*>(scale), mod_batch_stride,
+                   tokens_per_batch, static_cast<uint16_t*>(x_mod), x_mod_row_stride};
+  return FLK_OK;
+}
+
+int64_t row_blocks(const QuantProblem& p) { return ((int64_t)p.M + 3) / 4; }
 
 }  // namespace
 
@@ -727,32 +786,50 @@ extern "C" int flk_quantize_act(const void* x, int64_t x_row_stride, const float
   if (x_row_stride % 8 || !flk_host_aligned(x, 16) || !flk_host_aligned(inv_s, 16) || !flk_host_aligned(xq, 8) ||
       !flk_host_aligned(a_scale, 4))
     return FLK_E_ALIGN;
-  launch_quantize_act<false>((k / 8 + 63) / 64, dim3((unsigned)((m + 3) / 4)), as_stream(stream),
-                             static_cast<const uint16_t*>(x), x_row_stride, inv_s, m, k, xq, a_scale, nullptr,
-                             nullptr, 0, 1, nullptr, 0);
-  return flk_launch_status();
+  const QuantProblem p{static_cast<const uint16_t*>(x), x_row_stride, inv_s, m, xq, a_scale, nullptr, nullptr, 0, 1,
+                       nullptr, 0};
+  const int64_t blocks = row_blocks(p);
+  return launch_quantize_act<false>(QuantGroup{{p, p}, (int)std::min<int64_t>(blocks, INT32_MAX), k}, blocks,
+                                    stream);
 }
 
 extern "C" int flk_quantize_act_modulated(const void* x, int64_t x_row_stride, const void* shift,
                                           const void* scale, int64_t mod_batch_stride, int tokens_per_batch,
                                           const float* inv_s, int m, int k, int8_t* xq, float* a_scale,
                                           void* x_mod, int64_t x_mod_row_stride, void* stream) {
-  if (m < 0 || k < 0 || x_row_stride < k || tokens_per_batch <= 0 || mod_batch_stride < 0 ||
-      (x_mod && x_mod_row_stride < k))
-    return FLK_E_INVALID;
-  if (m == 0 || k == 0) return FLK_OK;
-  if (!x || !shift || !scale || !inv_s || !xq || !a_scale) return FLK_E_INVALID;
-  if ((m - 1) / tokens_per_batch > 0 && mod_batch_stride < k) return FLK_E_INVALID;
-  if (k % 8 || k > 8192) return FLK_E_UNSUPPORTED;
-  if (x_row_stride % 8 || mod_batch_stride % 8 || !flk_host_aligned(x, 16) || !flk_host_aligned(shift, 16) ||
-      !flk_host_aligned(scale, 16) || !flk_host_aligned(inv_s, 16) || !flk_host_aligned(xq, 8) ||
-      !flk_host_aligned(a_scale, 4) || (x_mod && (!flk_host_aligned(x_mod, 16) || x_mod_row_stride % 8)))
-    return FLK_E_ALIGN;
-  launch_quantize_act<true>((k / 8 + 63) / 64, dim3((unsigned)((m + 3) / 4)), as_stream(stream),
-                            static_cast<const uint16_t*>(x), x_row_stride, inv_s, m, k, xq, a_scale,
-                            static_cast<const uint16_t*>(shift), static_cast<const uint16_t*>(scale), mod_batch_stride,
-                            tokens_per_batch, static_cast<uint16_t*>(x_mod), x_mod_row_stride);
-  return flk_launch_status();
+  QuantProblem p{};
+  const int st = modulated_problem(x, x_row_stride, shift, scale, mod_batch_stride, tokens_per_batch, inv_s, m, k,
+                                   xq, a_scale, x_mod, x_mod_row_stride, p);
+  if (st != FLK_OK) return st == kNoWork ? FLK_OK : st;
+  const int64_t blocks = row_blocks(p);
+  return launch_quantize_act<true>(QuantGroup{{p, p}, (int)std::min<int64_t>(blocks, INT32_MAX), k}, blocks,
+                                   stream);
+}
+
+extern "C" int flk_quantize_act_modulated_pair(
+    const void* x0, int64_t x_row_stride0, const void* shift0, const void* scale0, int64_t mod_batch_stride0,
+    int tokens_per_batch0, const float* inv_s0, int m0, int8_t* xq0, float* a_scale0, void* x_mod0,
+    int64_t x_mod_row_stride0,
+    const void* x1, int64_t x_row_stride1, const void* shift1, const void* scale1, int64_t mod_batch_stride1,
+    int tokens_per_batch1, const float* inv_s1, int m1, int8_t* xq1, float* a_scale1, void* x_mod1,
+    int64_t x_mod_row_stride1, int k, void* stream) {
+  QuantGroup g{};
+  g.K = k;
+  const int st0 = modulated_problem(x0, x_row_stride0, shift0, scale0, mod_batch_stride0, tokens_per_batch0, inv_s0,
+                                    m0, k, xq0, a_scale0, x_mod0, x_mod_row_stride0, g.p[0]);
+  if (st0 != FLK_OK && st0 != kNoWork) return st0;
+  const int st1 = modulated_problem(x1, x_row_stride1, shift1, scale1, mod_batch_stride1, tokens_per_batch1, inv_s1,
+                                    m1, k, xq1, a_scale1, x_mod1, x_mod_row_stride1, g.p[1]);
+  if (st1 != FLK_OK && st1 != kNoWork) return st1;
+  if (st0 == kNoWork && st1 == kNoWork) return FLK_OK;
+  // An empty problem gives its place to the other one, which then takes every block.
+  if (st0 == kNoWork) g.p[0] = g.p[1];
+  if (st1 == kNoWork) g.p[1] = g.p[0];
+  const bool both = st0 == FLK_OK && st1 == FLK_OK;
+  const int64_t b0 = row_blocks(g.p[0]);
+  const int64_t blocks = both ? b0 + row_blocks(g.p[1]) : b0;
+  g.first_blocks = (int)std::min<int64_t>(b0, INT32_MAX);
+  return launch_quantize_act<true>(g, blocks, stream);
 }
 
 namespace {
@@ -769,7 +846,6 @@ int launch_group(const GemmGroup& g, int64_t blocks, void* stream) {
 
 // Checks one fused projection + qk_prep (flk_w8a8_qk_prep's arguments) and fills its
 // problem.  FLK_OK = launch, kNoWork = empty (nothing to launch), else an error status.
-constexpr int kNoWork = 1;
 
 int qk_problem(const int8_t* xq, const int8_t* wq_t, const float* a_scale, const float* w_scale, int k,
                const float* cos, const float* sin, int64_t table_row_stride, const void* q_scale,

@@ -141,6 +141,38 @@ def quantize_act_modulated(x: torch.Tensor, shift: torch.Tensor, scale: torch.Te
     x (B, L, K) bf16 block input; shift, scale (B, K) bf16 modulation rows (the reference's
     (B, 1, K) ``ModTriple`` entries).  Returns (xq (B*L, K) int8, a_scale (B*L,) f32), plus X
     (B, L, K) bf16 when ``x_mod`` is True or a tensor to write it into."""
+    xr, shift, scale, inv, xq, a_scale, out = _modulated_operands(x, shift, scale, inv_smooth, x_mod)
+    batch, length, k = x.shape
+    _lib.run("flk_quantize_act_modulated", (xr, shift, scale, inv, xq, a_scale, out),
+             xr.data_ptr(), xr.stride(0), shift.data_ptr(), scale.data_ptr(), shift.stride(0), length,
+             inv.data_ptr(), batch * length, k, xq.data_ptr(), a_scale.data_ptr(), _lib.ptr(out), k,
+             _lib.stream_of(x))
+    return (xq, a_scale) if out is None else (xq, a_scale, out)
+
+
+def quantize_act_modulated_pair(x0, shift0, scale0, inv_smooth0, x1, shift1, scale1, inv_smooth1):
+    """A double block's two modulated activations (text and image, each with its own
+    modulation rows and smoothing factors, same width) in one launch.  Returns
+    ((xq0, a_scale0), (xq1, a_scale1)), each exactly quantize_act_modulated of its stream."""
+    o0 = _modulated_operands(x0, shift0, scale0, inv_smooth0, None)
+    o1 = _modulated_operands(x1, shift1, scale1, inv_smooth1, None)
+    if x0.shape[2] != x1.shape[2]:
+        raise ValueError(f"both activations must have one width, got {x0.shape[2]} and {x1.shape[2]}")
+    _lib.run("flk_quantize_act_modulated_pair", (*o0[:6], *o1[:6]),
+             *_modulated_args(x0, *o0), *_modulated_args(x1, *o1), x0.shape[2], _lib.stream_of(x0))
+    return (o0[4], o0[5]), (o1[4], o1[5])
+
+
+def _modulated_args(x, xr, shift, scale, inv, xq, a_scale, out):
+    """One stream's arguments of flk_quantize_act_modulated_pair (x .. x_mod_row_stride)."""
+    batch, length, k = x.shape
+    return (xr.data_ptr(), xr.stride(0), shift.data_ptr(), scale.data_ptr(), shift.stride(0), length,
+            inv.data_ptr(), batch * length, xq.data_ptr(), a_scale.data_ptr(), _lib.ptr(out), k)
+
+
+def _modulated_operands(x, shift, scale, inv_smooth, x_mod):
+    """Checked device operands of one modulated activation: (x rows, shift, scale, 1/s, xq,
+    a_scale, X or None)."""
     if x.dim() != 3:
         raise ValueError(f"x must be (B, L, K), got {tuple(x.shape)}")
     batch, length, k = x.shape
@@ -163,10 +195,7 @@ def quantize_act_modulated(x: torch.Tensor, shift: torch.Tensor, scale: torch.Te
         out = x_mod
         if out.shape != (batch, length, k) or out.dtype != torch.bfloat16 or not out.is_contiguous():
             raise ValueError(f"x_mod must be a contiguous bfloat16 ({batch}, {length}, {k}) tensor")
-    _lib.run("flk_quantize_act_modulated", (xr, shift, scale, inv, xq, a_scale, out),
-             xr.data_ptr(), xr.stride(0), shift.data_ptr(), scale.data_ptr(), shift.stride(0), length,
-             inv.data_ptr(), m, k, xq.data_ptr(), a_scale.data_ptr(), _lib.ptr(out), k, _lib.stream_of(x))
-    return (xq, a_scale) if out is None else (xq, a_scale, out)
+    return xr, shift, scale, inv, xq, a_scale, out
 
 
 def gemm(xq: torch.Tensor, a_scale: torch.Tensor, wq_t: torch.Tensor, w_scale: torch.Tensor, *,
@@ -203,9 +232,10 @@ def linear(x: torch.Tensor, qw: QuantizedLinear, *, out: torch.Tensor | None = N
     return y.reshape(*lead, qw.out_features) if out is None else out
 
 
-def _qk_stream(x, qw: QuantizedLinear, q_scale, k_scale, freqs, num_heads: int, modulation):
+def _qk_stream(x, qw: QuantizedLinear, q_scale, k_scale, freqs, num_heads: int, modulation, quantized=None):
     """Checks and device operands of one fused projection + qk_prep stream: (xq, a_scale, cos,
-    sin, q_scale, k_scale, q_gain), the activation quantised (modulated first when given)."""
+    sin, q_scale, k_scale, q_gain), the activation quantised (modulated first when given)
+    unless ``quantized`` already holds its (xq, a_scale)."""
     from .kernels import HEAD_DIM, Freqs, PositionIds
 
     if x.dim() != 3:
@@ -229,7 +259,9 @@ def _qk_stream(x, qw: QuantizedLinear, q_scale, k_scale, freqs, num_heads: int, 
             or q_scale.numel() != HEAD_DIM or k_scale.numel() != HEAD_DIM:
         raise ValueError(f"q_scale / k_scale must be {HEAD_DIM} bfloat16 or float32 values of one dtype")
     q_scale, k_scale = q_scale.reshape(-1).contiguous(), k_scale.reshape(-1).contiguous()
-    if modulation is None:
+    if quantized is not None:
+        xq, a_scale = quantized
+    elif modulation is None:
         xq, a_scale = quantize_act(x, qw.inv_smooth)
     else:
         xq, a_scale = quantize_act_modulated(x, modulation[0], modulation[1], qw.inv_smooth)
@@ -290,9 +322,16 @@ def qk_prep_pair(txt, img, num_heads: int, *, out=None, modulation=None):
     bit-identical to ``qk_prep`` of that stream alone."""
     from .kernels import HEAD_DIM
 
-    mods = modulation if modulation is not None else (None, None)
-    s0 = _qk_stream(*txt, num_heads, mods[0])
-    s1 = _qk_stream(*img, num_heads, mods[1])
+    if modulation is not None and modulation[0] is not None and modulation[1] is not None:
+        (m0, m1) = modulation
+        q0, q1 = quantize_act_modulated_pair(txt[0], m0[0], m0[1], txt[1].inv_smooth,
+                                             img[0], m1[0], m1[1], img[1].inv_smooth)
+        s0 = _qk_stream(*txt, num_heads, None, quantized=q0)
+        s1 = _qk_stream(*img, num_heads, None, quantized=q1)
+    else:
+        mods = modulation if modulation is not None else (None, None)
+        s0 = _qk_stream(*txt, num_heads, mods[0])
+        s1 = _qk_stream(*img, num_heads, mods[1])
     x0, x1 = txt[0], img[0]
     if x0.shape[0] != x1.shape[0] or x0.shape[2] != x1.shape[2]:
         raise ValueError(f"text and image inputs must share batch and width, got {tuple(x0.shape)} "

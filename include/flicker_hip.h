@@ -201,6 +201,20 @@ int flk_quantize_act_modulated(const void* x, int64_t x_row_stride, const void* 
                                int64_t mod_batch_stride, int tokens_per_batch, const float* inv_s, int m, int k,
                                int8_t* xq, float* a_scale, void* x_mod, int64_t x_mod_row_stride, void* stream);
 
+/* Two flk_quantize_act_modulated activations of the same width k in one launch: a double
+ * block's text and image inputs, each with its own modulation rows and smoothing factors
+ * (modules.py:38-40 for img_mod and txt_mod, feeding the two projections of modules.py:
+ * 127-135).  The 512 text rows would otherwise be a small launch of their own.  Per stream
+ * the arguments and results are exactly flk_quantize_act_modulated's; an empty stream
+ * (m_i == 0) is skipped. */
+int flk_quantize_act_modulated_pair(const void* x0, int64_t x_row_stride0, const void* shift0, const void* scale0,
+                                    int64_t mod_batch_stride0, int tokens_per_batch0, const float* inv_s0, int m0,
+                                    int8_t* xq0, float* a_scale0, void* x_mod0, int64_t x_mod_row_stride0,
+                                    const void* x1, int64_t x_row_stride1, const void* shift1, const void* scale1,
+                                    int64_t mod_batch_stride1, int tokens_per_batch1, const float* inv_s1, int m1,
+                                    int8_t* xq1, float* a_scale1, void* x_mod1, int64_t x_mod_row_stride1, int k,
+                                    void* stream);
+
 /* y (m, n) bf16 = rescaled int8 product of xq (m, k) and wq_t (n, k); when acc_or_null is
  * given, the exact int32 products are also written there as (m, n).  k % 128 == 0,
  * n % 4 == 0, y 8-byte aligned with y_row_stride % 4 == 0. */

@@ -355,6 +355,30 @@ def test_fused_projection_pair_equals_two_calls(device, batch, len0, len1, heads
         assert bad == 0, f"{name}: {bad} of {a.numel()} elements differ"
 
 
+@pytest.mark.parametrize("batch,len0,len1,k", [(1, 512, 4096, 3072), (2, 7, 130, 200), (1, 0, 33, 256)])
+def test_modulated_activation_pair_equals_two_calls(device, batch, len0, len1, k):
+    """flk_quantize_act_modulated_pair: both streams' codes and scales equal their own
+    flk_quantize_act_modulated bit for bit (an empty text stream included)."""
+    g = torch.Generator().manual_seed(k + len1)
+    out = []
+    for n in (len0, len1):
+        x = (2.0 * torch.randn(batch, n, k, generator=g) + 0.3).to(torch.bfloat16).to(device)
+        shift = (0.5 * torch.randn(batch, k, generator=g)).to(torch.bfloat16).to(device)
+        scale = (0.2 * torch.randn(batch, k, generator=g)).to(torch.bfloat16).to(device)
+        inv_s = (0.5 + torch.rand(k, generator=g)).to(device)
+        out.append((x, shift, scale, inv_s))
+    got = w8a8.quantize_act_modulated_pair(*out[0], *out[1])
+    for (xq, a_scale), args in zip(got, out):
+        want_q, want_a = w8a8.quantize_act_modulated(*args)
+        torch.cuda.synchronize()
+        assert torch.equal(xq, want_q) and torch.equal(a_scale, want_a)
+    with pytest.raises(ValueError, match="one width"):
+        x_other = torch.zeros(batch, 4, k + 8, dtype=torch.bfloat16, device=device)
+        w8a8.quantize_act_modulated_pair(*out[0], x_other, out[1][1][:, :1].expand(batch, k + 8).contiguous(),
+                                         out[1][2][:, :1].expand(batch, k + 8).contiguous(),
+                                         torch.ones(k + 8, device=device))
+
+
 def test_errors(device):
     x = torch.zeros((4, 100), dtype=torch.bfloat16, device=device)
     with pytest.raises(Exception, match="status -3"):        # k % 8

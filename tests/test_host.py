@@ -281,6 +281,9 @@ def test_w8a8_validation(lib):
     assert pair(*stream(512, 0), *stream(4096, 600), *tail) == _lib.FLK_E_INVALID     # past out_length
     assert pair(*stream(512, 0, FAKE + 4), *stream(4096, 512), *tail) == _lib.FLK_E_ALIGN
     assert pair(*stream(0, 0), *stream(0, 0), *tail) == _lib.FLK_OK                  # both empty
+    qm = lib.flk_quantize_act_modulated
+    assert qm(FAKE, 3072, FAKE, FAKE, 3072, 0, FAKE, 0, 3072, FAKE, FAKE, None, 0, None) == _lib.FLK_OK   # 0 tokens
+    assert qm(FAKE, 3072, FAKE, FAKE, 3072, 0, FAKE, 8, 3072, FAKE, FAKE, None, 0, None) == _lib.FLK_E_INVALID
 
 
 def test_w8a8_python_errors():
