@@ -67,6 +67,26 @@ def double_attention(txt_qkv, img_qkv, txt_scales, img_scales, freqs: Freqs | Po
     return attn[:, :num_txt], attn[:, num_txt:]
 
 
+def double_attention_int8(txt_x, img_x, txt_qw, img_qw, txt_scales, img_scales, freqs: Freqs | PositionIds,
+                          num_heads: int, *, modulation=None):
+    """double_attention on the int8 path from the blocks' inputs: both streams' modulate +
+    int8 quantisation in one launch and both projections with their qk prep in another
+    (``w8a8.qk_prep_pair``, replacing modules.py:127-139), then the joint attention with
+    merge_heads fused (modules.py:157-158).  ``modulation`` is ((shift, scale) of txt_mod,
+    (shift, scale) of img_mod) or None for already-modulated inputs.  Returns (txt_attn,
+    img_attn), each (B, L_stream, H*D)."""
+    from . import w8a8
+    num_txt = txt_x.shape[1]
+    if isinstance(freqs, PositionIds):
+        from .rope import rope_lanes
+        freqs = rope_lanes(freqs.ids, freqs.q_gain, freqs.axes_dim, freqs.theta)
+    txt = (txt_x, txt_qw, *txt_scales, _slice(freqs, 0, num_txt))
+    img = (img_x, img_qw, *img_scales, _slice(freqs, num_txt, num_txt + img_x.shape[1]))
+    joint = w8a8.qk_prep_pair(txt, img, num_heads, modulation=modulation)
+    attn = attend_merged(*joint)
+    return attn[:, :num_txt], attn[:, num_txt:]
+
+
 def single_attention(linear1_out, q_scale, k_scale, freqs: Freqs | PositionIds, num_heads: int,
                      hidden: int):
     """modules.py:185-191 + 198 -- the qkv part of the fused linear1 output (a strided view,

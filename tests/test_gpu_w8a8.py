@@ -392,3 +392,29 @@ def test_errors(device):
                   torch.ones(8, device=device))
     with pytest.raises(ValueError, match="GPU"):
         w8a8.quantize_act(torch.zeros((4, 64), dtype=torch.bfloat16), torch.ones(64))
+
+
+def test_double_attention_int8_equals_step_by_step(device):
+    """modules.double_attention_int8 (paired quantisation, paired projection + qk_prep, one
+    joint attention) equals the int8 path run stream by stream into the joint buffer."""
+    from flicker_amd import kernels, modules
+    from flicker_amd.kernels import Freqs
+    heads, k, n_txt, n_img = 2, 256, 40, 200
+    txt_x, txt_qw, qs0, ks0, f0, _ = _fused_case(device, 1, n_txt, heads, k, torch.bfloat16, 0.25, seed=61)
+    img_x, img_qw, qs1, ks1, _, _ = _fused_case(device, 1, n_img, heads, k, torch.bfloat16, 0.25, seed=62)
+    from flicker_amd import rope
+    from oracle import path as P
+    freqs = rope.rope_lanes(P.sequence_ids(n_txt, 10, 20), 0.25, device=device)
+    g = torch.Generator().manual_seed(63)
+    mods = tuple(((0.3 * torch.randn(1, k, generator=g)).to(torch.bfloat16).to(device),
+                  (0.1 * torch.randn(1, k, generator=g)).to(torch.bfloat16).to(device)) for _ in range(2))
+    got_txt, got_img = modules.double_attention_int8(txt_x, img_x, txt_qw, img_qw, (qs0, ks0), (qs1, ks1), freqs,
+                                                     heads, modulation=mods)
+    joint = tuple(torch.empty(1, heads, n_txt + n_img, 128, dtype=torch.bfloat16, device=device) for _ in range(3))
+    cut = lambda a, b: Freqs(freqs.cos[a:b], freqs.sin[a:b], freqs.q_gain)  # noqa: E731
+    w8a8.qk_prep(txt_x, txt_qw, qs0, ks0, cut(0, n_txt), heads, out=joint, out_offset=0, modulation=mods[0])
+    w8a8.qk_prep(img_x, img_qw, qs1, ks1, cut(n_txt, n_txt + n_img), heads, out=joint, out_offset=n_txt,
+                 modulation=mods[1])
+    want = kernels.attend_merged(*joint)
+    torch.cuda.synchronize()
+    assert torch.equal(got_txt, want[:, :n_txt]) and torch.equal(got_img, want[:, n_txt:])
