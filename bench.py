@@ -299,13 +299,21 @@ def w8a8_leg(args, timed, dev) -> dict:
         def pair(i):
             w8a8.qk_prep_pair(txt, img, heads, out=qkv_out[i % 2], modulation=((shift, scale), (shift, scale)))
 
+        def section2(i):   # the whole double-block attention section on this path
+            from flicker_amd import modules
+            modules.double_attention_int8(txt[0], img[0], qw_txt, qw, (qs, ks), (qs, ks), freqs, heads,
+                                          modulation=((shift, scale), (shift, scale)))
+
         two(0)
         pair(0)
+        section2(0)
         double = {"text_tokens": n_txt, "image_tokens": p.tokens - n_txt,
                   "two_launches_us": round(timed(two, args.steps) * 1e3, 2),
                   "pair_us": round(timed(pair, args.steps) * 1e3, 2),
+                  "section_us": round(timed(section2, args.steps) * 1e3, 2),
                   "what": "modulate+quantise per stream, then the fused projection + qk_prep of both "
-                          "streams: two launches, or one (flk_w8a8_qk_prep_pair)"}
+                          "streams: two launches of each, or one (the _pair entry points); section_us "
+                          "adds the joint attend_merged (modules.double_attention_int8)"}
     del x3
     return {"workload": f"{p.name}: X ({p.tokens}, {p.hidden}) bf16 with {p.outlier_fraction:.0%} outlier "
                         f"channels x{p.outlier_gain:g}, W ({p.hidden}, {p.out_features}) ~ N(0, 0.02)",
