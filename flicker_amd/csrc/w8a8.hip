@@ -32,6 +32,10 @@
 // stores whole 256-byte output rows.  Blocks are renumbered so consecutive output tiles
 // share an XCD (and its L2), and grouped so that 4 token tiles sweep the channel tiles
 // together.
+//
+// A launch takes up to two problems (GemmGroup; the activation quantiser likewise takes a
+// QuantGroup): a double block's text and image projections share one grid, so the small
+// text projection runs on the CUs the image projection leaves idle in its last round.
 
 #include <algorithm>
 
