@@ -112,8 +112,13 @@ def device_of(*tensors) -> torch.device:
 def run(name: str, tensors, *args) -> None:
     """Call entry point ``name`` with the tensors' GPU current -- a HIP launch goes to the
     current device, whatever device the tensors live on -- and raise on a non-zero status."""
-    with torch.cuda.device(device_of(*tensors)):
-        check(getattr(lib(), name)(*args), name)
+    device = device_of(*tensors)
+    fn = getattr(lib(), name)
+    if torch.cuda.current_device() == device.index:
+        check(fn(*args), name)
+        return
+    with torch.cuda.device(device):
+        check(fn(*args), name)
 
 
 def ptr(t: torch.Tensor | None) -> int | None:
