@@ -40,6 +40,18 @@ def test_library_exports_every_declared_symbol(lib):
     assert lib.flk_abi_version() == _lib.ABI_VERSION
 
 
+def test_header_is_plain_c():
+    """include/flicker_hip.h is the FFI boundary (ctypes here; cgo or a C caller elsewhere): it
+    must parse as C99, not only as C++."""
+    import shutil
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        pytest.skip("no C compiler on this host")
+    proc = subprocess.run([cc, "-fsyntax-only", "-Wall", "-Wextra", "-Werror", "-std=c99", "-x", "c",
+                           os.path.join(ROOT, "include", "flicker_hip.h")], capture_output=True, text=True)
+    assert proc.returncode == 0, proc.stderr
+
+
 def test_status_strings(lib):
     for code in (_lib.FLK_OK, _lib.FLK_E_INVALID, _lib.FLK_E_ALIGN, _lib.FLK_E_UNSUPPORTED):
         assert _lib.status_string(code)
