@@ -5,9 +5,12 @@ attention on its output, at the Klein 4B 1024^2 shape by default (512 text + 64x
 image tokens = 4608, 24 heads x 128).  Inputs are resident in HBM before timing.
 
 The timed region is `--steps` steps (qk_prep then attend) between two HIP events on the
-launch stream (torch's current stream) -> ms_per_step.  Each kernel is then timed alone the
-same way, `--steps` back-to-back launches over the same rotating buffers, which gives its
-average launch duration: `value` is attend's TFLOP/s from that, and the line also reports
+launch stream (torch's current stream) -> ms_per_step.  Before it run `--warmup` untimed
+steps and then untimed steps for `--clock-warmup-s` seconds (reported as clock_warmup_s):
+the GPU takes about a second of load to reach its working clock, which a few warm-up steps
+do not give.  Each kernel is then timed alone the same way, `--kernel-launches`
+back-to-back launches over the same rotating buffers, which gives its average launch
+duration: `value` is attend's TFLOP/s from that, and the line also reports
 qk_prep's GB/s and both roofline fractions.  To keep the QKV input from being
 served by the 256 MB Infinity Cache between steps, steps rotate over buffer sets
 whose total exceeds it.  A CPU baseline (the torch-CPU restatement of the reference's
@@ -54,12 +57,19 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=300,
-                    help="untimed steps; enough (~0.1 s) to bring the GPU to its working clock")
+                    help="untimed steps before the timed region")
+    ap.add_argument("--clock-warmup-s", type=float, default=2.0,
+                    help="further untimed steps, for this many seconds, before the timed region: the "
+                         "GPU needs ~1 s of load to settle at its working clock whatever --warmup is; "
+                         "reported as clock_warmup_s (0 = off)")
+    ap.add_argument("--kernel-launches", type=int, default=200,
+                    help="back-to-back launches of each kernel alone behind its average launch duration")
     ap.add_argument("--workload", default="klein_1024")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-w8a8", action="store_true", help="skip the int8 W8A8 QKV projection leg")
     ap.add_argument("--projection", default="qkv_1024")
-    ap.add_argument("--cpu-reps", type=int, default=3)
+    ap.add_argument("--cpu-reps", type=int, default=9,
+                    help="timed CPU-baseline steps (after 3 warm-up steps); the p50 is reported")
     ap.add_argument("--only", choices=["step", "calibrate"], default="step",
                     help="calibrate: the step plus a plain device copy of known size, for counter runs")
     ap.add_argument("--ingest-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
@@ -158,16 +168,37 @@ def ingest_pmc(fetch_dir: str, write_dir: str, workload: str) -> dict:
     return out
 
 
+CPU_WARMUPS = 3   # the reference's method: 3 warm-up calls, then the p50 (tools/bench.py:21,25-33)
+
+
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), or the platform's processor string."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or "unknown"
+
+
 def cpu_baseline(w, qkv, qs, ks, ids, reps: int) -> dict:
-    """Time the oracle's torch-CPU plain path on the full step (all heads), p50 of `reps`."""
+    """Time the oracle's torch-CPU plain path on the full step (all heads): CPU_WARMUPS warm-up
+    steps, then the p50 of `reps` steps.  `cores` is the number of threads torch computes
+    with (the host's CPU share: OMP_NUM_THREADS where the launcher sets it), `host_cpus` the
+    CPUs this process may run on."""
     import torch
 
     from oracle import cpu_baseline as cb
     from oracle import path as P
 
     pe = torch.from_numpy(P.embed_nd(ids)[0, 0])
+    host_cpus = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
     threads = torch.get_num_threads()
-    cb.plain_attention(qkv, qs, ks, pe, w.num_heads, heads=[0])   # warm-up
+    for _ in range(CPU_WARMUPS):
+        cb.plain_attention(qkv, qs, ks, pe, w.num_heads)
     times = []
     for _ in range(reps):
         t0 = time.perf_counter()
@@ -176,9 +207,9 @@ def cpu_baseline(w, qkv, qs, ks, ids, reps: int) -> dict:
     times.sort()
     p50 = times[len(times) // 2]
     return {"value": round(w.attend_flops() / p50 / 1e12, 4), "unit": "TFLOP/s", "cores": threads,
-            "kind": "port", "ms": round(p50 * 1e3, 1),
-            "sample": f"full {w.name} step (qk norm+RoPE+sdpa, all {w.num_heads} heads, f32 torch CPU), "
-                      f"p50 of {reps} after 1 warm-up"}
+            "host_cpus": host_cpus, "cpu_model": cpu_model(), "kind": "port", "ms": round(p50 * 1e3, 1),
+            "sample": f"full {w.name} step (qk norm+RoPE+sdpa, all {w.num_heads} heads, f32 torch CPU on "
+                      f"{threads} threads), p50 of {reps} after {CPU_WARMUPS} warm-up steps"}
 
 
 def projection_operands(p, dev):
@@ -227,8 +258,8 @@ def w8a8_leg(args, timed, dev) -> dict:
     ys = [torch.empty((p.tokens, p.out_features), dtype=torch.bfloat16, device=dev) for _ in range(2)]
     for i in range(20):
         w8a8.gemm(xq, a_scale, qw.wq_t, qw.w_scale, out=ys[i % 2])
-    gemm_ms = timed(lambda i: w8a8.gemm(xq, a_scale, qw.wq_t, qw.w_scale, out=ys[i % 2]), args.steps)
-    quant_ms = timed(lambda i: w8a8.quantize_act(x, qw.inv_smooth), args.steps)
+    gemm_ms = timed(lambda i: w8a8.gemm(xq, a_scale, qw.wq_t, qw.w_scale, out=ys[i % 2]), args.kernel_launches)
+    quant_ms = timed(lambda i: w8a8.quantize_act(x, qw.inv_smooth), args.kernel_launches)
     tops = p.gemm_ops() / (gemm_ms * 1e-3) / 1e12
     # The projection feeding qk_prep: the GEMM + qk_prep pair, and the fused kernel whose
     # epilogue does qk_prep (flk_w8a8_qk_prep), on the projection's tokens as one sequence.
@@ -260,13 +291,13 @@ def w8a8_leg(args, timed, dev) -> dict:
         w8a8.gemm(xq, a_scale, qw.wq_t, qw.w_scale, out=y)
         kernels.qk_prep(y.view(1, p.tokens, p.out_features), qs, ks, freqs, heads, out=qkv_out[i % 2])
 
-    fused_ms = timed(fused, args.steps)
-    unfused_ms = timed(unfused, args.steps)
+    fused_ms = timed(fused, args.kernel_launches)
+    unfused_ms = timed(unfused, args.kernel_launches)
     # The block input's modulate (LayerNorm, scale, shift) fused into the quantisation.
     g = torch.Generator().manual_seed(6)
     shift = (0.3 * torch.randn(1, p.hidden, generator=g)).to(torch.bfloat16).to(dev)
     scale = (0.1 * torch.randn(1, p.hidden, generator=g)).to(torch.bfloat16).to(dev)
-    mod_ms = timed(lambda i: w8a8.quantize_act_modulated(x3, shift, scale, qw.inv_smooth), args.steps)
+    mod_ms = timed(lambda i: w8a8.quantize_act_modulated(x3, shift, scale, qw.inv_smooth), args.kernel_launches)
     # A block's whole attention section on this path (modules.py:128-133 + 157 for one stream):
     # modulate + int8 quantisation, the projection with qk_prep in its epilogue, attention
     # with merge_heads in its epilogue -- three launches.
@@ -278,7 +309,7 @@ def w8a8_leg(args, timed, dev) -> dict:
         kernels.attend_merged(*o, out=merged[i % 2])
 
     section(0)
-    section_ms = timed(section, args.steps)
+    section_ms = timed(section, args.kernel_launches)
     # A double block's two projections (modules.py:127-139): the first 512 tokens as the text
     # stream with its own weight, the rest as the image stream, each modulated, into one joint
     # q/k/v buffer -- two fused launches, or one for both (w8a8.qk_prep_pair).
@@ -308,9 +339,9 @@ def w8a8_leg(args, timed, dev) -> dict:
         pair(0)
         section2(0)
         double = {"text_tokens": n_txt, "image_tokens": p.tokens - n_txt,
-                  "two_launches_us": round(timed(two, args.steps) * 1e3, 2),
-                  "pair_us": round(timed(pair, args.steps) * 1e3, 2),
-                  "section_us": round(timed(section2, args.steps) * 1e3, 2),
+                  "two_launches_us": round(timed(two, args.kernel_launches) * 1e3, 2),
+                  "pair_us": round(timed(pair, args.kernel_launches) * 1e3, 2),
+                  "section_us": round(timed(section2, args.kernel_launches) * 1e3, 2),
                   "what": "modulate+quantise per stream, then the fused projection + qk_prep of both "
                           "streams: two launches of each, or one (the _pair entry points); section_us "
                           "adds the joint attend_merged (modules.double_attention_int8)"}
@@ -423,13 +454,24 @@ def main() -> int:
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
+    # Clock warm-up: untimed steps for a fixed time, so the timed region starts at the GPU's
+    # working clock whatever --warmup is (a few steps leave it ramping for ~1 s).
+    clock_t0 = time.perf_counter()
+    clock_steps = 0
+    while time.perf_counter() - clock_t0 < args.clock_warmup_s:
+        for _ in range(50):
+            step(clock_steps)
+            clock_steps += 1
+        torch.cuda.synchronize()
+    clock_warmup_s = time.perf_counter() - clock_t0 if clock_steps else 0.0
     step_ms = timed(step, args.steps)
     # Per-kernel launch durations: each kernel alone, back to back over the same rotating
     # buffers (what a rocprofv3 kernel trace of the same command reports per dispatch).
-    qk_ms = timed(run_qk, args.steps) if args.only == "step" else step_ms
-    at_ms = timed(run_attend, args.steps) if args.only == "step" else step_ms
+    n_kernel = args.kernel_launches
+    qk_ms = timed(run_qk, n_kernel) if args.only == "step" else step_ms
+    at_ms = timed(run_attend, n_kernel) if args.only == "step" else step_ms
     qk_gbs = w.qk_prep_bytes() / (qk_ms * 1e-3) / 1e9
-    qk_ids_ms = timed(run_qk_ids, args.steps) if args.only == "step" else None
+    qk_ids_ms = timed(run_qk_ids, n_kernel) if args.only == "step" else None
     at_tflops = w.attend_flops() / (at_ms * 1e-3) / 1e12
 
     def p50_launch_us(fn, reps: int = 30) -> float:
@@ -473,6 +515,9 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "clock_warmup_s": round(clock_warmup_s, 2),
+        "clock_warmup_steps": clock_steps,
+        "kernel_launches": n_kernel if args.only == "step" else None,
         "ms_per_step": round(step_ms, 4),
         "higher_is_better": True,
         "scaling": "weak",

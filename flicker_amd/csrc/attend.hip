@@ -538,7 +538,8 @@ extern "C" int flk_attend_split_to(const void* q, const void* k, const void* v, 
   if (!flk_host_aligned(workspace, 16)) return FLK_E_ALIGN;
   const int64_t units = q_tiles(length) * batch * heads;
   const int64_t total = units * splits;
-  if (total > INT32_MAX) return FLK_E_INVALID;
+  const int64_t merge_blocks = units * kWaves * 16 * 64 / kMergeThreads;
+  if (total > INT32_MAX || merge_blocks > INT32_MAX) return FLK_E_INVALID;
   float* part_acc = static_cast<float*>(workspace);
   float* part_l = part_acc + total * kThreads * 64;
   const hipStream_t hs = static_cast<hipStream_t>(stream);
@@ -548,8 +549,6 @@ extern "C" int flk_attend_split_to(const void* q, const void* k, const void* v, 
                      (int)total, heads, splits, o_batch_stride, o_head_stride, o_row_stride, part_acc, part_l);
   const int launched = flk_launch_status();
   if (launched != FLK_OK) return launched;
-  const int64_t merge_blocks = units * kWaves * 16 * 64 / kMergeThreads;
-  if (merge_blocks > INT32_MAX) return FLK_E_INVALID;
   hipLaunchKernelGGL(attend_merge_kernel, dim3((unsigned)merge_blocks), dim3(kMergeThreads), 0, hs, part_acc,
                      part_l, static_cast<uint16_t*>(o), length, (int)q_tiles(length), units, heads, splits,
                      o_batch_stride, o_head_stride, o_row_stride);

@@ -12,7 +12,7 @@ from __future__ import annotations
 
 import torch
 
-from .kernels import Freqs, PositionIds, _launch_qk_prep, attend_merged, lane_pair
+from .kernels import Freqs, PositionIds, _launch_qk_prep, attend_merged, lane_pair, row_tile
 
 
 def heads(qkv: torch.Tensor, num_heads: int):
@@ -31,13 +31,30 @@ def merge_heads(x: torch.Tensor) -> torch.Tensor:
 
 def qkv_prep(qkv, q_scale, k_scale, pe, freqs: Freqs | PositionIds | None, num_heads: int, *, out=None,
              out_offset: int = 0):
-    """modules.py:68-80 -- QK-RMSNorm + RoPE + head split.  The reference switches between its
-    fused kernel and a plain-XLA branch; here both are the one HIP kernel: without ``freqs``
-    the lane tables are built from ``pe`` with gain 1 (the plain branch applies no q_gain),
-    and any L is accepted (the plain branch has no row-tile condition)."""
-    if freqs is None:
-        freqs = lane_pair(pe, 1.0)
-    return _launch_qk_prep(qkv, q_scale, k_scale, freqs, num_heads, out, out_offset)
+    """modules.py:68-80 -- QK-RMSNorm + RoPE + head split, with the reference's gate (:76):
+    the fused form (``freqs``' lanes and ``freqs.q_gain``) when ``freqs`` is given and a row
+    tile divides L; otherwise the plain branch (:78-80), which rotates by ``pe`` and applies
+    no query gain.  Both branches run the one HIP kernel: the plain branch's lane tables are
+    built from ``pe`` at gain 1 (lane_pair), whose rotation is bit-identical to apply_rope's
+    2x2 form.  ``pe`` is (B_pe, 1, L, D/2, 2, 2); with B_pe > 1 each batch element is
+    rotated by its own table, as apply_rope broadcasts it."""
+    if freqs is not None and row_tile(qkv.shape[1]) is not None:
+        return _launch_qk_prep(qkv, q_scale, k_scale, freqs, num_heads, out, out_offset)
+    if pe is None:
+        raise ValueError(f"qkv_prep: L={qkv.shape[1]} has no row tile (or freqs is None), so the plain "
+                         "branch needs pe")
+    if pe.dim() < 6 or pe.shape[0] == 1:
+        return _launch_qk_prep(qkv, q_scale, k_scale, lane_pair(pe, 1.0), num_heads, out, out_offset)
+    batch = qkv.shape[0]
+    if pe.shape[0] != batch:
+        raise ValueError(f"pe batch {pe.shape[0]} does not broadcast against qkv batch {batch}")
+    if out is None:
+        shape = (batch, num_heads, qkv.shape[1], qkv.shape[2] // (3 * num_heads))
+        out = tuple(torch.empty(shape, dtype=torch.bfloat16, device=qkv.device) for _ in range(3))
+    for b in range(batch):
+        _launch_qk_prep(qkv[b:b + 1], q_scale, k_scale, lane_pair(pe[b:b + 1], 1.0), num_heads,
+                        tuple(t[b:b + 1] for t in out), out_offset)
+    return tuple(out)
 
 
 def _slice(freqs, start: int, stop: int):
@@ -49,19 +66,21 @@ def _slice(freqs, start: int, stop: int):
 
 
 def double_attention(txt_qkv, img_qkv, txt_scales, img_scales, freqs: Freqs | PositionIds,
-                     num_heads: int):
+                     num_heads: int, *, pe=None, pe_ctx=None):
     """modules.py:127-139 + 157-158 -- per-stream qk prep, joint text|image attention, merge,
     split back into (txt_attn, img_attn), each (B, L_stream, H*D).
 
     Both qk_prep calls write into one (B, H, L_txt + L_img, D) buffer at their sequence
-    offsets, which replaces the reference's three concatenations."""
+    offsets, which replaces the reference's three concatenations.  ``pe_ctx`` / ``pe`` are the
+    text / image rope tables the reference hands each stream's qkv_prep (modules.py:129,133);
+    they are read only by a stream whose length has no row tile (the gate's plain branch)."""
     batch, num_txt, width = txt_qkv.shape
     num_img = img_qkv.shape[1]
     head_dim = width // (3 * num_heads)
     shape = (batch, num_heads, num_txt + num_img, head_dim)
     joint = tuple(torch.empty(shape, dtype=torch.bfloat16, device=txt_qkv.device) for _ in range(3))
-    qkv_prep(txt_qkv, *txt_scales, None, _slice(freqs, 0, num_txt), num_heads, out=joint, out_offset=0)
-    qkv_prep(img_qkv, *img_scales, None, _slice(freqs, num_txt, num_txt + num_img), num_heads,
+    qkv_prep(txt_qkv, *txt_scales, pe_ctx, _slice(freqs, 0, num_txt), num_heads, out=joint, out_offset=0)
+    qkv_prep(img_qkv, *img_scales, pe, _slice(freqs, num_txt, num_txt + num_img), num_heads,
              out=joint, out_offset=num_txt)
     attn = attend_merged(*joint)   # merge_heads fused into the attention epilogue
     return attn[:, :num_txt], attn[:, num_txt:]
@@ -88,9 +107,10 @@ def double_attention_int8(txt_x, img_x, txt_qw, img_qw, txt_scales, img_scales, 
 
 
 def single_attention(linear1_out, q_scale, k_scale, freqs: Freqs | PositionIds, num_heads: int,
-                     hidden: int):
+                     hidden: int, *, pe=None):
     """modules.py:185-191 + 198 -- the qkv part of the fused linear1 output (a strided view,
-    consumed without a copy) -> qk prep -> attention -> merge; returns (attn, mlp)."""
+    consumed without a copy) -> qk prep -> attention -> merge; returns (attn, mlp).  ``pe``
+    is the joint sequence's rope table, read only by the gate's plain branch (no row tile)."""
     qkv, mlp = linear1_out[..., : 3 * hidden], linear1_out[..., 3 * hidden:]
-    q, k, v = qkv_prep(qkv, q_scale, k_scale, None, freqs, num_heads)
+    q, k, v = qkv_prep(qkv, q_scale, k_scale, pe, freqs, num_heads)
     return attend_merged(q, k, v), mlp

@@ -94,10 +94,6 @@ class Projection:
         """2 M K N integer multiply-adds counted as two ops each."""
         return 2 * self.tokens * self.hidden * self.out_features
 
-    def gemm_bytes(self) -> int:
-        """Algorithmic HBM bytes of one GEMM: int8 X and W once, bf16 Y written."""
-        return self.tokens * self.hidden + self.hidden * self.out_features + 2 * self.tokens * self.out_features
-
 
 PROJECTIONS = {p.name: p for p in (Projection("qkv_1024", 4608), Projection("qkv_512", 1536))}
 

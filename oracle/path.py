@@ -178,6 +178,15 @@ def qk_prep_fused(qkv, q_scale, k_scale, freqs: Freqs, num_heads, scale_is_bf16=
     return qo, ko, v.copy()
 
 
+def qkv_prep(qkv, q_scale, k_scale, pe, freqs: Freqs | None, num_heads, scale_is_bf16=True):
+    """modules.py:68-80 -- the dispatch gate: the fused kernel (kernels.py:57-91, with
+    ``freqs``' lanes and ``freqs.q_gain``) iff ``freqs`` is given and a row tile divides L
+    (:76-77); otherwise the plain branch (:78-80), rotating by ``pe`` with no query gain."""
+    if freqs is not None and row_tile(np.shape(qkv)[1]) is not None:
+        return qk_prep_fused(qkv, q_scale, k_scale, freqs, num_heads, scale_is_bf16)
+    return qk_prep_plain(qkv, q_scale, k_scale, pe, num_heads, scale_is_bf16)
+
+
 # ----------------------------------------------------------------------------- attention
 def _rows(length: int, chunk: int):
     for start in range(0, length, chunk):

@@ -76,15 +76,47 @@ def test_qk_prep_matches_oracle(device, batch, length, heads, gain):
 
 @pytest.mark.parametrize("length", [1, 17, 100, 4352])
 def test_qk_prep_ragged_length(device, length):
-    """Lengths that are not multiples of the 16-token block (through qkv_prep, which has no
-    row-tile condition, as the reference's plain branch)."""
+    """Lengths that are not multiples of the 16-token block, through qkv_prep: L = 1, 17 and
+    100 have no row tile and take the plain branch (lanes from pe), 4352 = 17 * 256 the fused
+    one; at gain 1 both compute the same values."""
     qkv, qs, ks, ids = make_case(1, length, 24, seed=length)
-    tables = oracle_tables(ids, 1.0)
-    got = modules.qkv_prep(qkv.to(device), qs.to(device), ks.to(device), None,
+    pe = P.embed_nd(ids)
+    tables = P.lane_pair(pe, 1.0)
+    got = modules.qkv_prep(qkv.to(device), qs.to(device), ks.to(device), torch.from_numpy(pe).to(device),
                            gpu_freqs(tables, device), 24)
     torch.cuda.synchronize()
     check_qkv(f"L{length}", got, P.qk_prep_fused(to_np(qkv), to_np(qs), to_np(ks), tables, 24,
                                                 return_normed=True), 1.0)
+
+
+@pytest.mark.parametrize("batch,length,pe_batch", [(1, 100, 1), (1, 257, 1), (2, 100, 2), (1, 256, 1)])
+def test_qkv_prep_gate(device, batch, length, pe_batch):
+    """modules.py:76-80 with the bounded path's q_gain = 1/sqrt(128): a length with no row tile
+    (100, 257) takes the plain branch -- rotation by pe, no gain -- and 256 the fused kernel
+    with the gain; each against the oracle's gate (oracle.path.qkv_prep).  pe with a batch
+    axis rotates each batch element by its own table (apply_rope broadcasts pe)."""
+    gain = 1 / math.sqrt(128)
+    qkv, qs, ks, ids = make_case(batch, length, 24, seed=900 + length + batch)
+    if pe_batch > 1:
+        g = np.random.default_rng(length)
+        ids = np.stack([ids] + [g.integers(0, 128, ids.shape).astype(np.float32) for _ in range(pe_batch - 1)])
+    pe = P.embed_nd(ids)
+    freqs = P.lane_pair(pe, gain)
+    got = modules.qkv_prep(qkv.to(device), qs.to(device), ks.to(device), torch.from_numpy(pe).to(device),
+                           gpu_freqs(freqs, device), 24)
+    torch.cuda.synchronize()
+    want = P.qkv_prep(to_np(qkv), to_np(qs), to_np(ks), pe, freqs, 24)
+    fused = P.row_tile(length) is not None
+    normed = P.qk_prep_fused(to_np(qkv), to_np(qs), to_np(ks), P.lane_pair(pe[:1], 1.0), 24,
+                             return_normed=True)[3:]
+    if pe_batch > 1:   # the normed rows do not depend on the table; q, k of batch b on pe[b]
+        for b in range(batch):
+            rows = P.qk_prep_fused(to_np(qkv)[b:b + 1], to_np(qs), to_np(ks), P.lane_pair(pe[b:b + 1], 1.0), 24)
+            assert all(np.array_equal(w[b:b + 1], r) for w, r in zip(want, rows))
+    check_qkv(f"gate B{batch} L{length} {'fused' if fused else 'plain'}", got, tuple(want) + tuple(normed),
+              gain if fused else 1.0)
+    rms = np.sqrt((to_np(got[0]).astype(np.float64) ** 2).mean(-1)).mean()
+    assert abs(rms - (gain if fused else 1.0)) < 0.05 * (gain if fused else 1.0), rms
 
 
 def test_qk_prep_f32_scales(device):

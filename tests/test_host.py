@@ -183,6 +183,21 @@ def test_python_errors_follow_the_reference():
                         kernels.Freqs(torch.zeros(128, 128), torch.zeros(128, 128)), 24)
 
 
+def test_qkv_prep_gate_host_side():
+    """modules.py:76-80: a length with no row tile takes the plain branch, which needs pe; with
+    pe it goes to the GPU kernel (so a CPU tensor is refused, there is no CPU branch)."""
+    from flicker_amd import modules
+    qkv = torch.zeros(1, 100, 9216, dtype=torch.bfloat16)
+    f = kernels.Freqs(torch.zeros(100, 128), torch.zeros(100, 128), 1 / math.sqrt(128))
+    with pytest.raises(ValueError, match="plain branch needs pe"):
+        modules.qkv_prep(qkv, torch.ones(128), torch.ones(128), None, f, 24)
+    pe = torch.from_numpy(P.embed_nd(np.zeros((100, 4), np.float32)))
+    with pytest.raises(ValueError, match="GPU"):
+        modules.qkv_prep(qkv, torch.ones(128), torch.ones(128), pe, f, 24)
+    with pytest.raises(ValueError, match="broadcast"):
+        modules.qkv_prep(qkv, torch.ones(128), torch.ones(128), torch.cat([pe] * 3), f, 24)
+
+
 def test_logit_bound_and_check_match_oracle():
     rng = np.random.default_rng(0)
     qs, ks = rng.standard_normal((2, 5, 128)).astype(np.float32)

@@ -170,6 +170,26 @@ def test_gain_is_applied_after_rotation_before_rounding():
     assert not np.array_equal(q_g, bf16_round((np.float32(gain) * q1).astype(np.float32)))
 
 
+def test_qkv_prep_gate_follows_row_tile():
+    """modules.py:76-80: the fused form (lanes and q_gain) iff freqs is given and a row tile
+    divides L, else the plain branch from pe with no gain.  Pinned by the rows' RMS: RoPE is
+    orthogonal, so with unit norm scales a prepared row has RMS 1 on the plain branch and RMS
+    q_gain on the fused one; k is never scaled."""
+    gain = 1 / math.sqrt(128)
+    ones = np.ones(128, np.float32)
+    for length, fused in ((11, False), (100, False), (257, False), (64, True), (128, True)):
+        qkv, _, _, ids = _case(7 + length, heads=2, length=length)
+        pe = P.embed_nd(ids)
+        for freqs in (P.lane_pair(pe, gain), None):
+            q, k, v = P.qkv_prep(qkv, ones, ones, pe, freqs, 2)
+            rms_q = np.sqrt((q.astype(np.float64) ** 2).mean(-1))
+            rms_k = np.sqrt((k.astype(np.float64) ** 2).mean(-1))
+            np.testing.assert_allclose(rms_k, 1.0, atol=1e-2)
+            want = gain if (fused and freqs is not None) else 1.0
+            np.testing.assert_allclose(rms_q, want, rtol=1e-2)
+            np.testing.assert_array_equal(v, P.heads(qkv, 2)[2])
+
+
 def test_qk_prep_invariants():
     qkv, qs, ks, ids = _case(6, heads=2, length=64)
     q, k, v = P.qk_prep_fused(qkv, np.ones(128, np.float32), np.ones(128, np.float32),
