@@ -196,8 +196,9 @@ def _ids_and_tables_paths(device, qkv, qs, ks, ids, heads, gain):
     ids_dev = torch.from_numpy(np.ascontiguousarray(ids, dtype=np.float32)).to(device)
     args = (qkv.to(device), qs.to(device), ks.to(device))
     freqs = rope.rope_lanes(ids_dev, gain)
-    via_ids = modules.qkv_prep(*args, None, rope.position_ids(ids_dev, gain), heads)
-    via_tables = modules.qkv_prep(*args, None, freqs, heads)
+    # the launch below kernels.qk_prep's row-tile check, so that any L reaches the kernel
+    via_ids = kernels._launch_qk_prep(*args, rope.position_ids(ids_dev, gain), heads, None, 0)
+    via_tables = kernels._launch_qk_prep(*args, freqs, heads, None, 0)
     torch.cuda.synchronize()
     return via_ids, via_tables, P.Freqs(to_np(freqs.cos), to_np(freqs.sin), gain)
 
