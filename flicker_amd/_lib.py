@@ -28,6 +28,7 @@ SIGNATURES = {
     "flk_attend": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _p]),
     "flk_attend_to": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _i64, _i64, _i64, _p]),
     "flk_attend_split_to": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _i64, _i64, _i64, _i, _p, _i64, _p]),
+    "flk_attend_split_static_to": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _i64, _i64, _i64, _i, _p]),
     "flk_attend_plan": (_i, [_i, _i, _i, _ip, ctypes.POINTER(ctypes.c_int64)]),
     "flk_rope_embed": (_i, [_p, _i64, _i64, _i, _ip, _f, _p, _p]),
     "flk_lane_pair": (_i, [_p, _i64, _i, _p, _p, _p]),
@@ -49,7 +50,8 @@ SIGNATURES = {
 }
 
 ABI_VERSION = 1
-FLK_OK, FLK_E_INVALID, FLK_E_ALIGN, FLK_E_UNSUPPORTED = 0, -1, -2, -3
+FLK_OK, FLK_E_INVALID, FLK_E_ALIGN, FLK_E_UNSUPPORTED, FLK_E_SCRATCH = 0, -1, -2, -3, -4
+ATTEND_STATIC_SCRATCH_BYTES = 34078720   # FLK_ATTEND_STATIC_SCRATCH_BYTES
 
 
 class HipLibraryMissing(RuntimeError):

@@ -52,8 +52,16 @@
 // divides.  With no running max the partial sums need no rescaling.
 
 #include <algorithm>
+#include <mutex>
 
 #include "common.h"
+
+// Fixed partials buffer of flk_attend_split_static_to (device memory beyond its inputs and
+// outputs, so that callers which cannot allocate can still take the key-split path).  Each
+// GPU the library runs on holds its own copy until the process ends.  In host code this name
+// is only a stand-in for the symbol: its device address is looked up per device with
+// hipGetSymbolAddress (static_scratch below) and only that address reaches a kernel.
+static __device__ __align__(256) uint8_t scratch[FLK_ATTEND_STATIC_SCRATCH_BYTES];
 
 namespace {
 
@@ -523,23 +531,23 @@ extern "C" int flk_attend_plan(int batch, int heads, int length, int* splits, in
   return FLK_OK;
 }
 
-extern "C" int flk_attend_split_to(const void* q, const void* k, const void* v, void* o, int batch, int heads,
-                                   int length, int head_dim, int64_t o_batch_stride, int64_t o_head_stride,
-                                   int64_t o_row_stride, int splits, void* workspace, int64_t workspace_bytes,
-                                   void* stream) {
-  const int st = check_attend(q, k, v, o, batch, heads, length, head_dim, o_batch_stride, o_head_stride,
-                              o_row_stride);
-  if (st != FLK_OK) return st == kNothing ? FLK_OK : st;
-  if (splits < 1 || splits > key_groups(length)) return FLK_E_INVALID;
-  if (splits == 1) return launch_attend(q, k, v, o, batch, heads, length, o_batch_stride, o_head_stride,
-                                        o_row_stride, stream);
-  const int64_t need = split_workspace_bytes(batch, heads, length, splits);
-  if (!workspace || workspace_bytes < need) return FLK_E_INVALID;
-  if (!flk_host_aligned(workspace, 16)) return FLK_E_ALIGN;
+namespace {
+
+// Grid sizes of a split launch, checked before anything is launched.
+int check_split_grid(int batch, int heads, int length, int splits) {
   const int64_t units = q_tiles(length) * batch * heads;
   const int64_t total = units * splits;
   const int64_t merge_blocks = units * kWaves * 16 * 64 / kMergeThreads;
-  if (total > INT32_MAX || merge_blocks > INT32_MAX) return FLK_E_INVALID;
+  return total > INT32_MAX || merge_blocks > INT32_MAX ? FLK_E_INVALID : FLK_OK;
+}
+
+// The split kernel into `workspace` (at least split_workspace_bytes), then the merge.
+int launch_split(const void* q, const void* k, const void* v, void* o, int batch, int heads, int length,
+                 int64_t o_batch_stride, int64_t o_head_stride, int64_t o_row_stride, int splits,
+                 void* workspace, void* stream) {
+  const int64_t units = q_tiles(length) * batch * heads;
+  const int64_t total = units * splits;
+  const int64_t merge_blocks = units * kWaves * 16 * 64 / kMergeThreads;
   float* part_acc = static_cast<float*>(workspace);
   float* part_l = part_acc + total * kThreads * 64;
   const hipStream_t hs = static_cast<hipStream_t>(stream);
@@ -553,4 +561,77 @@ extern "C" int flk_attend_split_to(const void* q, const void* k, const void* v, 
                      part_l, static_cast<uint16_t*>(o), length, (int)q_tiles(length), units, heads, splits,
                      o_batch_stride, o_head_stride, o_row_stride);
   return flk_launch_status();
+}
+
+// Device address of `scratch` on the GPU that runs `stream`, looked up once per device with
+// that device current and kept for the life of the process.
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_addr[kMaxDevices] = {};
+
+int static_scratch(void* stream, void** addr) {
+  int cur = 0;
+  hipError_t e = hipGetDevice(&cur);
+  if (e != hipSuccess) return (int)e;
+  hipDevice_t dev = cur;
+  if (stream) {
+    e = hipStreamGetDevice(static_cast<hipStream_t>(stream), &dev);
+    if (e != hipSuccess) return (int)e;
+  }
+  if (dev < 0 || dev >= kMaxDevices) return FLK_E_UNSUPPORTED;
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_addr[dev]) {
+    if (dev != cur && (e = hipSetDevice(dev)) != hipSuccess) return (int)e;
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (dev != cur) {
+      const hipError_t back = hipSetDevice(cur);
+      if (e == hipSuccess && back != hipSuccess) e = back;
+    }
+    if (e != hipSuccess) return (int)e;
+    g_scratch_addr[dev] = p;
+  }
+  *addr = g_scratch_addr[dev];
+  return FLK_OK;
+}
+
+}  // namespace
+
+extern "C" int flk_attend_split_to(const void* q, const void* k, const void* v, void* o, int batch, int heads,
+                                   int length, int head_dim, int64_t o_batch_stride, int64_t o_head_stride,
+                                   int64_t o_row_stride, int splits, void* workspace, int64_t workspace_bytes,
+                                   void* stream) {
+  const int st = check_attend(q, k, v, o, batch, heads, length, head_dim, o_batch_stride, o_head_stride,
+                              o_row_stride);
+  if (st != FLK_OK) return st == kNothing ? FLK_OK : st;
+  if (splits < 1 || splits > key_groups(length)) return FLK_E_INVALID;
+  if (splits == 1) return launch_attend(q, k, v, o, batch, heads, length, o_batch_stride, o_head_stride,
+                                        o_row_stride, stream);
+  const int64_t need = split_workspace_bytes(batch, heads, length, splits);
+  if (!workspace || workspace_bytes < need) return FLK_E_INVALID;
+  if (!flk_host_aligned(workspace, 16)) return FLK_E_ALIGN;
+  const int grid = check_split_grid(batch, heads, length, splits);
+  if (grid != FLK_OK) return grid;
+  return launch_split(q, k, v, o, batch, heads, length, o_batch_stride, o_head_stride, o_row_stride, splits,
+                      workspace, stream);
+}
+
+extern "C" int flk_attend_split_static_to(const void* q, const void* k, const void* v, void* o, int batch,
+                                          int heads, int length, int head_dim, int64_t o_batch_stride,
+                                          int64_t o_head_stride, int64_t o_row_stride, int splits, void* stream) {
+  const int st = check_attend(q, k, v, o, batch, heads, length, head_dim, o_batch_stride, o_head_stride,
+                              o_row_stride);
+  if (st != FLK_OK) return st == kNothing ? FLK_OK : st;
+  if (splits < 1 || splits > key_groups(length)) return FLK_E_INVALID;
+  if (splits == 1) return launch_attend(q, k, v, o, batch, heads, length, o_batch_stride, o_head_stride,
+                                        o_row_stride, stream);
+  if (split_workspace_bytes(batch, heads, length, splits) > (int64_t)FLK_ATTEND_STATIC_SCRATCH_BYTES)
+    return FLK_E_SCRATCH;
+  const int grid = check_split_grid(batch, heads, length, splits);
+  if (grid != FLK_OK) return grid;
+  void* ws = nullptr;
+  const int found = static_scratch(stream, &ws);
+  if (found != FLK_OK) return found;
+  return launch_split(q, k, v, o, batch, heads, length, o_batch_stride, o_head_stride, o_row_stride, splits,
+                      ws, stream);
 }

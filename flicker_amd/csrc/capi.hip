@@ -12,6 +12,7 @@ extern "C" const char* flk_status_string(int status) {
     case FLK_E_INVALID: return "invalid argument (size, count or offset out of range)";
     case FLK_E_ALIGN: return "pointer or stride not 16-byte aligned";
     case FLK_E_UNSUPPORTED: return "unsupported shape (the kernels take head_dim 128 only)";
+    case FLK_E_SCRATCH: return "the call needs more than the library's fixed scratch buffer holds";
     default: break;
   }
   if (status > 0) return hipGetErrorString(static_cast<hipError_t>(status));

@@ -24,6 +24,7 @@ extern "C" {
 #define FLK_E_INVALID (-1)     /* a size, count or offset out of range          */
 #define FLK_E_ALIGN (-2)       /* a pointer or stride breaks the 16-byte rule    */
 #define FLK_E_UNSUPPORTED (-3) /* a shape the library has no kernel for        */
+#define FLK_E_SCRATCH (-4)     /* needs more than a fixed scratch buffer holds  */
 
 /* ABI revision of this header (bumped on any signature change). */
 int flk_abi_version(void);
@@ -119,6 +120,28 @@ int flk_attend_split_to(const void* q, const void* k, const void* v, void* o,
                         int batch, int heads, int length, int head_dim,
                         int64_t o_batch_stride, int64_t o_head_stride, int64_t o_row_stride,
                         int splits, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * flk_attend_split_to without a caller workspace: it allocates nothing (no hipMalloc, no
+ * allocating library call).  No counterpart in the reference; it is for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that forbid it).
+ * The partials live in a fixed device buffer of FLK_ATTEND_STATIC_SCRATCH_BYTES per GPU,
+ * held from the first call on that GPU until the process ends: enough for every split that
+ * flk_attend_plan picks (at most 256 (b, h, 256-query tile, range) blocks of 133120 bytes).
+ *   - A call whose workspace (as flk_attend_split_to's) would exceed the buffer returns
+ *     FLK_E_SCRATCH before anything is launched; splits == 1 needs no buffer.
+ *   - Every call on one GPU shares that GPU's buffer: calls that overlap on one GPU (on
+ *     different streams, or from different threads) race and must be ordered by the caller.
+ *     Nothing in the buffer has to start at zero.
+ *   - The first call on a GPU looks up the buffer's device address with that GPU current
+ *     (the GPU of `stream`, or the current one for the NULL stream).
+ * Other arguments and results as flk_attend_split_to, bit for bit.
+ */
+#define FLK_ATTEND_STATIC_SCRATCH_BYTES 34078720
+int flk_attend_split_static_to(const void* q, const void* k, const void* v, void* o,
+                               int batch, int heads, int length, int head_dim,
+                               int64_t o_batch_stride, int64_t o_head_stride, int64_t o_row_stride,
+                               int splits, void* stream);
 
 /*
  * The split count flk_attend_split_to should use for a shape, and its workspace size.

@@ -53,7 +53,7 @@ def test_header_is_plain_c():
 
 
 def test_status_strings(lib):
-    for code in (_lib.FLK_OK, _lib.FLK_E_INVALID, _lib.FLK_E_ALIGN, _lib.FLK_E_UNSUPPORTED):
+    for code in (_lib.FLK_OK, _lib.FLK_E_INVALID, _lib.FLK_E_ALIGN, _lib.FLK_E_UNSUPPORTED, _lib.FLK_E_SCRATCH):
         assert _lib.status_string(code)
     assert "unsupported" in _lib.status_string(_lib.FLK_E_UNSUPPORTED)
 
@@ -98,6 +98,29 @@ def test_attend_split_plan_and_validation(lib):
     with pytest.raises(_lib.HipKernelError):
         _lib.check(lib.flk_attend_plan(1, -1, 10, ctypes.byref(ctypes.c_int()), ctypes.byref(ctypes.c_int64())),
                    "flk_attend_plan")
+
+
+def test_attend_split_static_validation(lib):
+    """flk_attend_split_static_to refuses, before launching anything, split counts out of range
+    and calls whose partials would not fit its fixed buffer; every split flk_attend_plan picks
+    does fit."""
+    f = lib.flk_attend_split_static_to
+    hd = 3 * 128
+    args = (FAKE, FAKE, FAKE, FAKE, 1, 3, 4608, 128, 4608 * hd, 128, hd)
+    assert f(*args, 0, None) == _lib.FLK_E_INVALID
+    assert f(*args, 19, None) == _lib.FLK_E_INVALID
+    assert f(FAKE, FAKE, FAKE, FAKE, 1, 24, 16896, 128, 0, 16896 * 128, 128, 2, None) == _lib.FLK_E_SCRATCH
+    assert f(FAKE, FAKE, FAKE, FAKE, 1, 2, 4608, 128, 0, 4608 * 128, 128, 8, None) == _lib.FLK_E_SCRATCH
+    assert f(FAKE, FAKE, FAKE, FAKE + 4, 1, 3, 4608, 128, 0, 4608 * 128, 128, 4, None) == _lib.FLK_E_ALIGN
+    assert "scratch" in _lib.status_string(_lib.FLK_E_SCRATCH)
+    header = open(os.path.join(ROOT, "include", "flicker_hip.h")).read()
+    assert int(re.search(r"#define FLK_ATTEND_STATIC_SCRATCH_BYTES (\d+)", header).group(1)) == \
+        _lib.ATTEND_STATIC_SCRATCH_BYTES == 256 * 512 * 65 * 4
+    for b in (1, 2):
+        for h in range(1, 25):
+            for length in (64, 257, 1536, 4352, 4608, 16896):
+                _, nbytes = _lib.attend_plan(b, h, length)
+                assert nbytes <= _lib.ATTEND_STATIC_SCRATCH_BYTES, (b, h, length, nbytes)
 
 
 def test_qk_prep_validation(lib):
