@@ -7,28 +7,37 @@
 //   l += f32(P);  acc += P * v_j                       (f32)
 //   o_i = bf16(acc / l)
 //
-// Formulation.  Each wave owns 32 queries and computes the transposed score tile
-// S^T = K Q^T with v_mfma_f32_32x32x16_bf16 (A = K rows from LDS, B = Q^T held in
-// registers for the whole kernel).  In the 32x32 accumulator layout a lane owns one query
-// column and 16 key rows, so
-//   * exp / bf16 rounding / the row sum l are lane-local (l is reduced across the two
-//     lane halves once, in the epilogue), and
-//   * the rounded P registers are directly the B operand (keys x queries) of the second
-//     product O^T += V^T P^T -- no shuffle of P through LDS.
-// V stays row-major in LDS; its transposed operand (d rows x 8 keys per lane) is fetched
+// Formulation.  Each wave owns 32 queries, as two groups of 16, and computes the transposed
+// score tile S^T = K Q^T with v_mfma_f32_16x16x32_bf16 (A = 16 K rows x 32 d from LDS, B =
+// Q^T of one query group, held in registers for the whole kernel).  Under random bf16 data the
+// chip runs at its power limit, and at that limit the 16x16x32 form does the same flops on
+// less energy than 32x32x16 (a quarter of the accumulator traffic per instruction): with this
+// kernel's softmax mix it issues ~7% more flops per second (microbenchmark).  Each K operand
+// feeds the MFMAs of both query groups, so LDS traffic per flop is that of a 32-query 32x32
+// tile.  In the 16x16 accumulator layout lane l owns query l % 16 of its group and keys
+// 4(l/16) .. +3 of a 16-key tile, so
+//   * exp / bf16 rounding are lane-local, and
+//   * the rounded P of the unit's two 16-key tiles are directly the B operand (32 keys x 16
+//     queries) of O^T += V^T P^T, with k-slots 0-3 = keys 4(l/16) .. +3 and 4-7 = the same
+//     keys + 16 -- no shuffle of P through LDS.
+// The row sum l = sum f32(P) is one more MFMA per query group and unit: O^T's d tiles get a
+// ninth, whose A operand is a register constant with ones in row 0 and zeros elsewhere, so
+// its row 0 accumulates sum_k 1 * P[k] (exact products, f32 sums on the matrix pipe).  That
+// replaces 8 v_dot2 per phase: 2 cheap MFMAs (mostly-zero operand, no LDS read) in place of
+// a fifth of the VALU work, measured 3.6% faster.
+// V stays row-major in LDS; its transposed operand (16 d rows x 8 keys per lane) is fetched
 // with two ds_read_b64_tr_b16, whose 16-lane transpose hands lane 4a+b element b of source
-// lanes a, a+4, a+8, a+12 -- so source lane s points at key K0 + s/4, columns D0 + 4(s%4).
-// The 8 keys a lane receives follow the accumulator-row order of S^T, so the P registers
-// of lane half g line up with the V^T k-slots of the same half.
+// lanes a, a+4, a+8, a+12 -- so source lane s of lane group h points at key 4h + s/4 (then
+// 16 more), columns D0 + 4(s%4): the k-slots line up with those of P.
 //
-// Schedule.  Keys are processed in units of 32 (one S^T accumulator).  Phase u issues 16
-// MFMAs -- the 8 of S(u+1) = K(u+1) Q^T, then the 8 of O^T += V(u-1)^T P(u-1)^T -- and
-// spreads the exp work of unit u over them, one element per MFMA (log2(e) multiply of
-// element n+2, exp of n+1, and on every second slot the bf16 pack of a pair); the row sum
-// of the unit's packed pairs follows the phase's last MFMA as one run of v_dot2.  At two
-// waves per SIMD that VALU load mostly hides under the matrix pipe.  Each MFMA's LDS
-// operand is read kLead slots ahead into an 8-deep register ring, and the packed P values
-// are tied to their slots so the compiler cannot batch them elsewhere.
+// Schedule.  Keys are processed in units of 32 (two 16-key tiles).  Phase u issues 32 MFMAs
+// in 16 operand slots of two (one per query group) -- slots 0-7 the 16 of S(u+1) = K(u+1)
+// Q^T, slots 8-15 the 16 of O^T += V(u-1)^T P(u-1)^T -- and spreads the exp work of unit u
+// over the slots, one element per slot (log2(e) multiply of element n+2, exp of n+1, and on
+// every second slot the bf16 pack of a pair), and the two row-sum MFMAs follow the last d
+// tile.  At two waves per SIMD that VALU load mostly hides under the matrix pipe.  Each slot's LDS operand is read kLead slots ahead into an
+// 8-deep register ring, and the packed P values are tied to their slots so the compiler cannot
+// batch them elsewhere.
 //
 // Staging.  K and V live in separate 4-deep rings of 64-key tiles (16 KiB each).
 // Iteration t (the exp work of units 2t, 2t+1) reads K tiles t, t+1 and V tiles t-1, t,
@@ -36,9 +45,13 @@
 // started one iteration earlier, then a block barrier.  Copies go from global memory straight into LDS with
 // global_load_lds_dwordx4 (no registers), issued from inline asm so the compiler does not
 // order later LDS reads behind them: lane i of a wave instruction lands at M0 + 16 i, so
-// the XOR swizzle chunk' = chunk ^ swz(row), swz = ((row&3)<<1)|((row>>2)&1), is applied by
-// choosing which global chunk each lane fetches.  It keeps every 8 consecutive K rows (b128
-// operand reads) and every group of 4 V rows x 2 chunks (transpose reads) on distinct banks.
+// the XOR swizzle chunk' = chunk ^ swz(row), swz = ((row&7)<<1)|((row>>3)&1), is applied by
+// choosing which global chunk each lane fetches.  gfx950's LDS serves 256 B per clock from 64
+// banks, i.e. one whole 256-byte row: a b128 read is served 16 lanes at a time and a b64
+// transpose read 32 lanes at a time.  The swizzle puts the 16 K rows of a b128 operand read
+// (one chunk each) and the 8 V rows x 2 chunks of 32 lanes of a transpose read on 16 distinct
+// chunk positions, so neither read conflicts.  (A 3-bit swizzle, distinct over 8 rows only,
+// left both 2-way conflicted: SQ_LDS_BANK_CONFLICT counted exactly the predicted 2x.)
 // The main loop is unrolled over the four ring positions, so every LDS address is a
 // per-lane constant plus an immediate offset.
 //
@@ -74,7 +87,11 @@ constexpr int kThreads = kWaves * 64;
 constexpr int kRowBytes = kD * 2;        // one K or V row: 256 B = 16 chunks of 16 B
 constexpr int kUnitBytes = 32 * kRowBytes;
 constexpr int kTileBytes = kBN * kRowBytes;
-constexpr int kVRing = kRing * kTileBytes;     // byte offset of the V ring
+// The V ring sits at LDS offset 0 and the K ring above it.  K operand pointers leave out the
+// K ring's base, which the per-lane offsets k_off carry, so that every LDS address is a
+// per-lane register plus an immediate below 64 KiB (the DS offset field is 16 bits).
+constexpr int kVRing = 0;                      // byte offset of the V ring
+constexpr int kKRing = kRing * kTileBytes;     // byte offset of the K ring
 constexpr int kSmemBytes = 2 * kRing * kTileBytes;
 constexpr int kRowsPerWave = kBN / kWaves;     // tile rows each wave copies (8)
 constexpr int kDmaPerTensor = kRowsPerWave / 4;  // copy instructions per wave per tile (2)
@@ -87,89 +104,111 @@ constexpr int kOpRing = 8;               // operand registers in flight (> kLead
 static_assert(16 % kOpRing == 0 && kOpRing > kLead, "operand ring must divide 16 and exceed kLead");
 constexpr float kLog2e = 1.4426950408889634f;
 
-using flk::bf16x2;
 using flk::bf16x8;
-using flk::f32x16;
 using flk::f32x4;
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef short s16x8 __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
-__device__ __forceinline__ int swz(int row) { return ((row & 3) << 1) | ((row >> 2) & 1); }
+__device__ __forceinline__ int swz(int row) { return ((row & 7) << 1) | ((row >> 3) & 1); }
 
 struct WaveState {
-  bf16x8 qreg[8];      // Q^T operand, d step st
-  f32x16 oacc[4];      // O^T, d block m
-  f32x16 sA, sB;       // S^T of consecutive units
-  uint32_t pA[8], pB[8];  // bf16x2-packed P of consecutive units
-  bf16x8 ops[kOpRing]; // operand ring: the A operand of MFMA slot n sits in ops[n % kOpRing]
-  float lsum;
-  int k_off[4];        // K operand byte offsets within a unit, d steps 0-3 (step st + 4 is
-                       // 8 chunks = 128 B further: the swizzle only permutes the low 3 chunk bits)
-  int v_off[4];        // V^T transpose-read byte offsets within a unit (d block m), key step 0
+  bf16x8 qreg[4][2];   // Q^T operand: d step s (32 d), query group g (16 queries)
+  f32x4 oacc[8][2];    // O^T: d tile dt (16 d), query group g
+  f32x4 sA[4], sB[4];  // S^T of consecutive units, accumulator g * 2 + kt (16-key tile kt)
+  uint32_t pA[8], pB[8];  // bf16x2-packed P of consecutive units: word g * 4 + kt * 2 + pair
+  bf16x8 ops[kOpRing]; // operand ring: the A operand of slot n sits in ops[n % kOpRing]
+  f32x4 lacc[2];       // row sums l of query groups 0 and 1 (register 0 of lanes 0-15)
+  bf16x8 ones;         // A operand of the row-sum MFMA: row 0 all ones, rows 1-15 zero
+  int k_off[4];        // K operand byte offsets within a unit, d steps 0-3 (key tile 1 is 16 rows
+                       // further, with the same swizzle)
+  int v_off[8];        // V^T transpose-read byte offsets within a unit, d tiles 0-7
 };
 
+// The V^T operand of one 16-row d tile: keys 4h + (0..3) from the first transpose read and
+// keys 16 + 4h + (0..3) from the second (h = lane / 16).
 __device__ __forceinline__ bf16x8 v_operand(const uint8_t* vunit, int off) {
   const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vunit + off));
-  const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vunit + off + 8 * kRowBytes));
+  const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vunit + off + 16 * kRowBytes));
   const s16x8 both = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
   return __builtin_bit_cast(bf16x8, both);
 }
 
-// Slot n of a phase issues one MFMA: n < 8 is step n of S = K Q^T (A = K row operand of
-// d step n), n >= 8 is step i = n - 8 of O^T += V^T P^T (A = V^T operand of key step i / 4,
-// d block i % 4).  Its A operand is read from LDS kLead slots earlier.
+// Slot n of a phase issues two MFMAs, one per query group, sharing its A operand: n < 8 is
+// d step n / 2 of S = K Q^T for 16-key tile n % 2 (A = K rows of that tile and d step), n >= 8
+// is d tile n - 8 of O^T += V^T P^T (A = V^T operand of the tile).  The operand is read from
+// LDS kLead slots earlier.
 __device__ __forceinline__ bf16x8 load_operand(const WaveState& w, int n, const uint8_t* k_unit,
                                                const uint8_t* v_unit) {
-  if (n < 8) return *reinterpret_cast<const bf16x8*>(k_unit + w.k_off[n & 3] + (n >> 2) * 128);
-  const int i = n - 8;
-  return v_operand(v_unit, w.v_off[i & 3] + (i >> 2) * 16 * kRowBytes);
+  if (n < 8) {
+    const int st = n >> 1, kt = n & 1;
+    return *reinterpret_cast<const bf16x8*>(k_unit + w.k_off[st] + kt * 16 * kRowBytes);
+  }
+  const int dt = n - 8;
+  return v_operand(v_unit, w.v_off[dt]);
+}
+
+__device__ __forceinline__ f32x4 mfma16(const bf16x8& a, const bf16x8& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// P^T of query group g as the B operand of O^T += V^T P^T: k-slots 0-3 from 16-key tile 0,
+// 4-7 from tile 1 -- the group's four packed words, in order.
+__device__ __forceinline__ bf16x8 p_operand(const uint32_t (&p)[8], int g) {
+  return __builtin_bit_cast(bf16x8, make_uint4(p[4 * g], p[4 * g + 1], p[4 * g + 2], p[4 * g + 3]));
 }
 
 // Phase u: S(u+1) = K(u+1) Q^T and O^T += V(u-1)^T P(u-1)^T on the MFMA pipe, while the VALU
 // turns S(u) into P(u) and l.  k_cur / v_cur hold K(u+1) and V(u-1); k_next holds K(u+2),
 // whose first kLead operands (those of the next phase) are read at the end of this one.
+// Element n of a unit is register n % 4 of accumulator n / 4 = g * 2 + kt.
 template <bool kMask>
-__device__ __forceinline__ void phase(WaveState& w, const f32x16& s_cur, f32x16& s_next,
+__device__ __forceinline__ void phase(WaveState& w, const f32x4 (&s_cur)[4], f32x4 (&s_next)[4],
                                       const uint32_t (&p_prev)[8], uint32_t (&p_cur)[8],
                                       const uint8_t* k_cur, const uint8_t* v_cur, const uint8_t* k_next,
-                                      int key_base, int length, int g) {
-  f32x16 sv = s_cur;
-  asm volatile("" : "+v"(sv));
+                                      int key_base, int length, int h) {
+  f32x4 sv[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    sv[i] = s_cur[i];
+    asm volatile("" : "+v"(sv[i]));
+  }
   float t[16], e[16];
-  auto mul = [&](int n) { t[n] = sv[n] * kLog2e; };
+  auto mul = [&](int n) { t[n] = sv[n >> 2][n & 3] * kLog2e; };
   auto ex = [&](int n) { e[n] = __builtin_amdgcn_exp2f(t[n]); };
   auto pack = [&](int n) {  // elements n, n+1 -> p_cur[n/2]
     float e0 = e[n], e1 = e[n + 1];
     if constexpr (kMask) {
-      const int key0 = key_base + (n >> 2) * 8 + g * 4 + (n & 3);
+      const int key0 = key_base + ((n >> 2) & 1) * 16 + h * 4 + (n & 3);
       e0 = key0 < length ? e0 : 0.0f;
       e1 = key0 + 1 < length ? e1 : 0.0f;
     }
     p_cur[n >> 1] = flk::pack_bf16x2(e0, e1);
     asm volatile("" : "+v"(p_cur[n >> 1]));   // keep the pack in its MFMA slot
   };
-  auto rowsum = [&](int j) {  // l += both halves of p_cur[j]
-    const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
-    w.lsum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, p_cur[j]), ones, w.lsum, false);
-    asm volatile("" : "+v"(w.lsum));   // pinned here: l feeds only the epilogue, so it would sink
-  };
-  const bf16x8 pb0 = __builtin_bit_cast(bf16x8, make_uint4(p_prev[0], p_prev[1], p_prev[2], p_prev[3]));
-  const bf16x8 pb1 = __builtin_bit_cast(bf16x8, make_uint4(p_prev[4], p_prev[5], p_prev[6], p_prev[7]));
+  const bf16x8 pb0 = p_operand(p_prev, 0);
+  const bf16x8 pb1 = p_operand(p_prev, 1);
 
   mul(0);
   mul(1);
   ex(0);
-  s_next = f32x16{};
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int n = 0; n < 16; ++n) {
     bf16x8& a = w.ops[n % kOpRing];
     if (n < 8) {
-      s_next = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, w.qreg[n], s_next, 0, 0, 0);
+      const int st = n >> 1, kt = n & 1;
+      // each S chain starts from the MFMA's inline zero accumulator
+      s_next[kt] = mfma16(a, w.qreg[st][0], st == 0 ? f32x4{} : s_next[kt]);
+      s_next[2 + kt] = mfma16(a, w.qreg[st][1], st == 0 ? f32x4{} : s_next[2 + kt]);
     } else {
-      const int i = n - 8;
-      w.oacc[i & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, (i >> 2) ? pb1 : pb0, w.oacc[i & 3], 0, 0, 0);
+      const int dt = n - 8;
+      w.oacc[dt][0] = mfma16(a, pb0, w.oacc[dt][0]);
+      w.oacc[dt][1] = mfma16(a, pb1, w.oacc[dt][1]);
+      if (dt == 7) {
+        w.lacc[0] = mfma16(w.ones, pb0, w.lacc[0]);
+        w.lacc[1] = mfma16(w.ones, pb1, w.lacc[1]);
+      }
     }
     const int nl = n + kLead;   // slot whose operand is read now
     if (nl < 16) w.ops[nl % kOpRing] = load_operand(w, nl, k_cur, v_cur);
@@ -179,11 +218,6 @@ __device__ __forceinline__ void phase(WaveState& w, const f32x16& s_cur, f32x16&
     if (n & 1) pack(n - 1);
     __builtin_amdgcn_sched_barrier(0);
   }
-  // The row sum of the unit's 8 packed pairs, in pair order, after the phase's last MFMA:
-  // v_dot2 stalls the matrix pipe when it issues between MFMAs, and one run of eight here
-  // measured 2% faster than one dot2 per slot pair (same operations, same order, same bits).
-#pragma unroll
-  for (int j = 0; j < 8; ++j) rowsum(j);
 }
 
 // Copy 64-key tile `tile` (clamped to the last one) of K or V into an LDS ring slot.
@@ -213,7 +247,7 @@ struct Ctx {
   uint8_t* smem;
   const uint16_t* kh;
   const uint16_t* vh;
-  int length, ntiles, g;
+  int length, ntiles, h;
   CopyPlan cp;
 };
 
@@ -224,16 +258,16 @@ struct Ctx {
 // per-lane constant plus an immediate offset.
 template <bool kMask>
 __device__ __forceinline__ void iteration(WaveState& w, const Ctx& c, int t, int r) {
-  copy_tile(c.smem + ((r + 3) & 3) * kTileBytes, c.kh, t + 3, c.cp);
+  copy_tile(c.smem + kKRing + ((r + 3) & 3) * kTileBytes, c.kh, t + 3, c.cp);
   copy_tile(c.smem + kVRing + ((r + 2) & 3) * kTileBytes, c.vh, t + 2, c.cp);
-  const uint8_t* k_t = c.smem + r * kTileBytes;                          // K tile t
-  const uint8_t* k_t1 = c.smem + ((r + 1) & 3) * kTileBytes;             // K tile t+1
+  const uint8_t* k_t = c.smem + r * kTileBytes;                          // K tile t (less kKRing)
+  const uint8_t* k_t1 = c.smem + ((r + 1) & 3) * kTileBytes;             // K tile t+1 (less kKRing)
   const uint8_t* v_t = c.smem + kVRing + r * kTileBytes;                 // V tile t
   const uint8_t* v_tm1 = c.smem + kVRing + ((r + 3) & 3) * kTileBytes;   // V tile t-1
   const int key0 = t * kBN;
   // phase 2t: K(2t+1), V(2t-1), next K(2t+2); phase 2t+1: K(2t+2), V(2t), next K(2t+3)
-  phase<kMask>(w, w.sA, w.sB, w.pB, w.pA, k_t + kUnitBytes, v_tm1 + kUnitBytes, k_t1, key0, c.length, c.g);
-  phase<kMask>(w, w.sB, w.sA, w.pA, w.pB, k_t1, v_t, k_t1 + kUnitBytes, key0 + 32, c.length, c.g);
+  phase<kMask>(w, w.sA, w.sB, w.pB, w.pA, k_t + kUnitBytes, v_tm1 + kUnitBytes, k_t1, key0, c.length, c.h);
+  phase<kMask>(w, w.sB, w.sA, w.pA, w.pB, k_t1, v_t, k_t1 + kUnitBytes, key0 + 32, c.length, c.h);
   // Wait for the copies started one iteration ago, then a plain s_barrier: the LDS reads
   // still in flight touch no buffer the next copies write, so no lgkmcnt wait is needed.
   asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" :: "n"(kDmaPerIter) : "memory");
@@ -270,8 +304,8 @@ __global__ __launch_bounds__(kThreads, 2) void attend_kernel(
   const int wave = tid >> 6, lane = tid & 63;
   Ctx c;
   c.smem = smem;
-  c.g = lane >> 5;            // lane half: selects k-slots 8g..8g+7 and accumulator rows 4g..
-  const int col = lane & 31;  // query column (S^T, O^T) / operand row (K, V^T)
+  c.h = lane >> 4;            // lane group: k-slots 8h..8h+7 and accumulator rows 4h..4h+3
+  const int col = lane & 15;  // query column (S^T, O^T) / operand row (K, V^T) in a 16-tile
   c.length = length;
   c.ntiles = (length + kBN - 1) / kBN;
   c.cp.last_tile = c.ntiles - 1;
@@ -299,38 +333,51 @@ __global__ __launch_bounds__(kThreads, 2) void attend_kernel(
 
   // Prologue copies: K tiles t_begin .. +2, V tiles t_begin .. +1 into ring slots 0-2 and 0-1
   // (tile t sits in slot (t - t_begin) % 4).
-  for (int tl = 0; tl < 3; ++tl) copy_tile(smem + tl * kTileBytes, c.kh, t_begin + tl, c.cp);
+  for (int tl = 0; tl < 3; ++tl) copy_tile(smem + kKRing + tl * kTileBytes, c.kh, t_begin + tl, c.cp);
   for (int tl = 0; tl < 2; ++tl) copy_tile(smem + kVRing + tl * kTileBytes, c.vh, t_begin + tl, c.cp);
 
   WaveState w;
-  const int q0 = qblk * kBM + wave * 32;
-  const int qi = q0 + col;
+  const int q0 = qblk * kBM + wave * 32;   // query group g of this wave: q0 + 16 g .. + 15
+  // k-slots 8h..8h+7 of the S MFMAs take d chunk dperm = 4 st + perm(h) of the K and Q rows,
+  // perm(h) = 0, 2, 1, 3: lanes l and l + 32 then read neighbouring chunks (c, c ^ 1), which
+  // the swizzle keeps on distinct banks whether a b128 read is served as 16 consecutive lanes
+  // or as 8 lanes from each half of the wave.
+  const int hperm = ((c.h & 1) << 1) | (c.h >> 1);
 #pragma unroll
-  for (int s = 0; s < 8; ++s) {
-    w.qreg[s] = qi < length ? *reinterpret_cast<const bf16x8*>(qh + (int64_t)qi * kD + s * 16 + c.g * 8)
-                            : bf16x8{};
+  for (int g = 0; g < 2; ++g) {
+    const int qi = q0 + g * 16 + col;
+#pragma unroll
+    for (int st = 0; st < 4; ++st)
+      w.qreg[st][g] = qi < length
+                          ? *reinterpret_cast<const bf16x8*>(qh + (int64_t)qi * kD + st * 32 + hperm * 8)
+                          : bf16x8{};
   }
 #pragma unroll
-  for (int m = 0; m < 4; ++m) w.oacc[m] = f32x16{};
-  w.lsum = 0.0f;
+  for (int dt = 0; dt < 8; ++dt) w.oacc[dt][0] = w.oacc[dt][1] = f32x4{};
+  w.lacc[0] = w.lacc[1] = f32x4{};
+  {
+    const __bf16 one = (lane & 15) == 0 ? (__bf16)1.0f : (__bf16)0.0f;
+    w.ones = bf16x8{one, one, one, one, one, one, one, one};
+  }
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    w.k_off[s] = col * kRowBytes + ((((s << 1) | c.g) ^ swz(col)) << 4);
-    asm volatile("" : "+v"(w.k_off[s]));
+  for (int st = 0; st < 4; ++st) {
+    // K operand of d step st: row col of the 16-key tile, d = 32 st + 8 perm(h) .. +7
+    w.k_off[st] = kKRing + col * kRowBytes + ((((st << 2) | hperm) ^ swz(col)) << 4);
+    asm volatile("" : "+v"(w.k_off[st]));
   }
   {
-    // Transpose-read source lane: 16-lane block h, lane sl in it -> key g*4 + sl/4 (+16 ks,
-    // +8 for the upper four k-slots), columns m*32 + 16*(h&1) + 4*(sl&3) .. +3.
-    const int h = lane >> 4, sl = lane & 15;
-    const int key = c.g * 4 + (sl >> 2);
+    // Transpose-read source lane sl of lane group h -> key 4h + sl/4 (+16 for k-slots 4-7),
+    // columns 16 dt + 4 (sl % 4) .. +3: chunk 2 dt + (sl % 4) / 2, half sl % 2.
+    const int sl = lane & 15;
+    const int key = c.h * 4 + (sl >> 2);
     const int half = sl & 1;
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      const int chunk = 4 * m + 2 * (h & 1) + ((sl & 3) >> 1);
-      w.v_off[m] = key * kRowBytes + ((chunk ^ swz(key)) << 4) + half * 8;
+    for (int dt = 0; dt < 8; ++dt) {
+      const int chunk = 2 * dt + ((sl & 3) >> 1);
+      w.v_off[dt] = key * kRowBytes + ((chunk ^ swz(key)) << 4) + half * 8;
       // Opaque to the compiler: it then adds the (immediate) unit offsets with the DS
       // instruction's offset field instead of a v_or per read.
-      asm volatile("" : "+v"(w.v_off[m]));
+      asm volatile("" : "+v"(w.v_off[dt]));
     }
   }
 #pragma unroll
@@ -342,11 +389,12 @@ __global__ __launch_bounds__(kThreads, 2) void attend_kernel(
   __syncthreads();
 
   // S(0) from K unit 0; operands of phase 0: K(1) and a placeholder V (multiplied by P(-1) = 0).
-  w.sA = f32x16{};
 #pragma unroll
-  for (int st = 0; st < 8; ++st) {
-    const bf16x8 a = *reinterpret_cast<const bf16x8*>(smem + w.k_off[st & 3] + (st >> 2) * 128);
-    w.sA = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, w.qreg[st], w.sA, 0, 0, 0);
+  for (int n = 0; n < 8; ++n) {
+    const int st = n >> 1, kt = n & 1;
+    const bf16x8 a = load_operand(w, n, smem, smem);
+    w.sA[kt] = mfma16(a, w.qreg[st][0], st == 0 ? f32x4{} : w.sA[kt]);
+    w.sA[2 + kt] = mfma16(a, w.qreg[st][1], st == 0 ? f32x4{} : w.sA[2 + kt]);
   }
 #pragma unroll
   for (int n = 0; n < kLead; ++n) w.ops[n % kOpRing] = load_operand(w, n, smem + kUnitBytes, smem);
@@ -368,43 +416,50 @@ __global__ __launch_bounds__(kThreads, 2) void attend_kernel(
   // Drain: O^T += V(U-1)^T P(U-1)^T for the last unit (unit 1 of the last tile).
   {
     const uint8_t* v_last = smem + kVRing + ((t_end - 1 - t_begin) & 3) * kTileBytes + kUnitBytes;
-    const bf16x8 pb0 = __builtin_bit_cast(bf16x8, make_uint4(w.pB[0], w.pB[1], w.pB[2], w.pB[3]));
-    const bf16x8 pb1 = __builtin_bit_cast(bf16x8, make_uint4(w.pB[4], w.pB[5], w.pB[6], w.pB[7]));
+    const bf16x8 pb0 = p_operand(w.pB, 0);
+    const bf16x8 pb1 = p_operand(w.pB, 1);
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-      w.oacc[i & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(load_operand(w, 8 + i, v_last, v_last),
-                                                              (i >> 2) ? pb1 : pb0, w.oacc[i & 3], 0, 0, 0);
+    for (int dt = 0; dt < 8; ++dt) {
+      const bf16x8 a = load_operand(w, 8 + dt, v_last, v_last);
+      w.oacc[dt][0] = mfma16(a, pb0, w.oacc[dt][0]);
+      w.oacc[dt][1] = mfma16(a, pb1, w.oacc[dt][1]);
+    }
+    w.lacc[0] = mfma16(w.ones, pb0, w.lacc[0]);
+    w.lacc[1] = mfma16(w.ones, pb1, w.lacc[1]);
   }
 
-  // Epilogue: l over both lane halves, O = bf16(acc / l), 4 d values per 8-byte store.
-  const float l = w.lsum + __shfl_xor(w.lsum, 32);
+  // Epilogue: l of each query group from lanes 0-15 (row 0 of the row-sum tile) to the lanes
+  // of every lane group, O = bf16(acc / l), 4 d values per 8-byte store.
+  float l[2];
+#pragma unroll
+  for (int g = 0; g < 2; ++g) l[g] = __shfl(w.lacc[g][0], lane & 15);
   if constexpr (kSplit) {
     // Partials in the accumulator's own lane order, so each store is 64 lanes x 16 bytes
-    // contiguous: with unit = bh * q_blocks + qblk, register group i = 4m + r holds
-    // acc[d = 32m + 8r + 4g .. +3] of query qi at float4 index
+    // contiguous: with unit = bh * q_blocks + qblk, register group i = 2 dt + g holds
+    // acc[d = 16 dt + 4h .. +3] of query q0 + 16 g + col at float4 index
     //   ((split * units + unit) * 8 + wave) * 1024 + i * 64 + lane,
-    // and l at ((split * units + unit) * 8 + wave) * 64 + lane.
+    // and the l of wave query j (= 16 g + col) at ((split * units + unit) * 8 + wave) * 64 + j.
     const int64_t units = total_blocks / splits;
     const int64_t slot = ((int64_t)split * units + (int64_t)bh * q_blocks + qblk) * kWaves + wave;
     f32x4* dst = reinterpret_cast<f32x4*>(part_acc) + slot * 1024 + lane;
 #pragma unroll
-    for (int m = 0; m < 4; ++m)
+    for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        dst[(m * 4 + r) * 64] = f32x4{w.oacc[m][r * 4 + 0], w.oacc[m][r * 4 + 1], w.oacc[m][r * 4 + 2],
-                                      w.oacc[m][r * 4 + 3]};
-    part_l[slot * 64 + lane] = l;
-  } else if (qi < length) {
-    const int b = bh / heads, h = bh - b * heads;
-    uint16_t* orow = o + b * o_batch_stride + h * o_head_stride + (int64_t)qi * o_row_stride;
+      for (int g = 0; g < 2; ++g) dst[(dt * 2 + g) * 64] = w.oacc[dt][g];
+    if (c.h < 2) part_l[slot * 64 + lane] = l[c.h];   // lanes 0-15: group 0, 16-31: group 1
+  } else {
+    const int b = bh / heads, hd = bh - b * heads;
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
+    for (int g = 0; g < 2; ++g) {
+      const int qi = q0 + g * 16 + col;
+      if (qi >= length) continue;
+      uint16_t* orow = o + b * o_batch_stride + hd * o_head_stride + (int64_t)qi * o_row_stride;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int d0 = m * 32 + r * 8 + c.g * 4;
+      for (int dt = 0; dt < 8; ++dt) {
+        const int d0 = dt * 16 + c.h * 4;
         uint2 val;
-        val.x = flk::pack_bf16x2(w.oacc[m][r * 4 + 0] / l, w.oacc[m][r * 4 + 1] / l);
-        val.y = flk::pack_bf16x2(w.oacc[m][r * 4 + 2] / l, w.oacc[m][r * 4 + 3] / l);
+        val.x = flk::pack_bf16x2(w.oacc[dt][g][0] / l[g], w.oacc[dt][g][1] / l[g]);
+        val.y = flk::pack_bf16x2(w.oacc[dt][g][2] / l[g], w.oacc[dt][g][3] / l[g]);
         *reinterpret_cast<uint2*>(orow + d0) = val;
       }
     }
@@ -434,17 +489,18 @@ __global__ __launch_bounds__(kMergeThreads) void attend_merge_kernel(
   if (unit >= units) return;
   const int64_t bh = unit / q_blocks;
   const int qblk = (int)(unit - bh * q_blocks);
-  const int qi = qblk * kBM + wave * 32 + (lane & 31);
+  const int qw = (i & 1) * 16 + (lane & 15);   // query within the wave: group i % 2, column lane % 16
+  const int qi = qblk * kBM + wave * 32 + qw;
   if (qi >= length) return;
   f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
   float l = 0.0f;
 #pragma unroll 4
   for (int s = 0; s < splits; ++s) {
     acc += reinterpret_cast<const f32x4*>(part_acc)[s * units * 8192 + id];
-    l += part_l[(s * units + unit) * 512 + wave * 64 + lane];
+    l += part_l[(s * units + unit) * 512 + wave * 64 + qw];
   }
   const int64_t b = bh / heads, h = bh - b * heads;
-  const int d0 = (i >> 2) * 32 + (i & 3) * 8 + (lane >> 5) * 4;
+  const int d0 = (i >> 1) * 16 + (lane >> 4) * 4;
   uint2 val;
   val.x = flk::pack_bf16x2(acc.x / l, acc.y / l);
   val.y = flk::pack_bf16x2(acc.z / l, acc.w / l);
