@@ -21,14 +21,18 @@
 // row stride; optional acc (M, N) int32.
 //
 // GEMM.  A block of 8 waves (two per SIMD) owns a 256 (n) x 256 (m) output tile and
-// computes it transposed, Y^T = WqT . Xq^T, with v_mfma_i32_32x32x32_i8: A operand = 32 WqT
-// rows x 32 k bytes, B operand = 32 Xq rows x 32 k bytes, both one ds_read_b128 per lane.
-// In the 32x32 accumulator a lane owns one token and 4 x 4 consecutive output channels.
-// Each wave holds a 128 (n) x 64 (m) sub-tile: 8 accumulators of 16 int32 (128 registers),
-// 6 operand reads per 8 MFMAs.  k advances in 128-byte stages (one full 128-byte line per
-// operand row) through two 64 KiB LDS buffers filled by global_load_lds_dwordx4 (no
-// registers); a row's 16-byte chunk c is stored at c ^ gswz(row), which keeps the 8- and
-// 16-lane phases of an operand read on distinct banks.  The epilogue rescales into LDS and
+// computes it transposed, Y^T = WqT . Xq^T, with v_mfma_i32_16x16x64_i8: A operand = 16 WqT
+// rows x 64 k bytes, B operand = 16 Xq rows x 64 k bytes, both one ds_read_b128 per lane.
+// Under random int8 data the chip runs at its power limit, where the 16x16x64 form does the
+// same ops on less energy than 32x32x32 (a quarter of the accumulator traffic per
+// instruction; an MFMA stream with random operands issues 12-17% more ops per second).  In
+// the 16x16 accumulator a lane owns one token and 4 consecutive output channels.  Each wave
+// holds a 128 (n) x 64 (m) sub-tile: 32 accumulators of 4 int32 (128 registers), 12 operand
+// reads per 32 MFMAs.  k advances in 128-byte stages (one full 128-byte line per operand
+// row) through two 64 KiB LDS buffers filled by global_load_lds_dwordx4 (no registers); a
+// row's 16-byte chunk c is stored at c ^ gswz(row), which keeps every operand read on
+// distinct banks.  Integer sums are exact in any order, so the products are those of any
+// other tiling, bit for bit.  The epilogue rescales into LDS and
 // stores whole 256-byte output rows.  Blocks are renumbered so consecutive output tiles
 // share an XCD (and its L2), and grouped so that 4 token tiles sweep the channel tiles
 // together.
@@ -375,47 +379,54 @@ constexpr int kGHalf = kGT * kGK;        // one operand's stage: 32 KiB
 constexpr int kGStage = 2 * kGHalf;      // WqT rows, then Xq rows; two stages fill 128 KiB
 constexpr int kGWaves = 8;               // two waves per SIMD
 constexpr int kGThreads = kGWaves * 64;
-constexpr int kGWaveN = 128;             // a wave's output channels (4 fragments of 32)
-constexpr int kGWaveM = 64;              // a wave's tokens (2 fragments of 32)
-constexpr int kGMT = kGWaveM / 32;
+constexpr int kGWaveN = 128;             // a wave's output channels (8 fragments of 16)
+constexpr int kGWaveM = 64;              // a wave's tokens (4 fragments of 16)
+constexpr int kGNF = kGWaveN / 16;       // channel fragments per wave
+constexpr int kGMF = kGWaveM / 16;       // token fragments per wave
 constexpr int kGCopies = kGT / kGWaves / 8;   // copy instructions per operand per wave and stage (4)
-constexpr int kGFrags = 4 + kGMT;             // operand fragments per k step: 4 WqT + 2 Xq
+constexpr int kGRing = 4;                // channel-fragment registers in flight
+constexpr int kGLead = 3;                // groups between a channel fragment's read and its MFMAs
+static_assert(kGNF % kGRing == 0 && kGRing > kGLead, "the fragment ring must divide the groups of a step");
 #ifndef FLK_GEMM_GROUP
 #define FLK_GEMM_GROUP 4
 #endif
 constexpr int kGroup = FLK_GEMM_GROUP;   // token tiles that sweep the channel tiles together
 constexpr int kXcds = 8;
 
-// LDS slot of 16-byte chunk c in row r is c ^ gswz(r).  An operand read takes chunk
-// 2 ks + half of rows r0 .. r0+31 (one row per lane): every 8 consecutive rows land on 8
-// distinct 16-byte slots of a 128-byte bank line, and every 16 consecutive rows on 16
-// distinct (row parity, slot) pairs, so neither 8-lane nor 16-lane read phases collide.
+// LDS slot of 16-byte chunk c in row r is c ^ gswz(r).  gfx950's LDS serves 256 B per clock
+// from 64 banks, i.e. two 128-byte operand rows; a b128 read is served as lanes 0-7 with
+// 32-39, 8-15 with 40-47, and so on.  An operand read takes rows r0 .. r0+15 (lane % 16) and
+// chunks 4 ks + perm(lane / 16), perm = 0, 2, 1, 3: lanes l and l + 32 then read chunks c and
+// c ^ 1 of the same 8 rows, which the swizzle spreads over the 16 slots of a bank line (as it
+// does the 16 rows of lanes l .. l + 15).
 __device__ __forceinline__ int gswz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
 
-__device__ __forceinline__ const uint8_t* frag_base(const uint8_t* stage, int i, int wn, int wm) {
-  return i < 4 ? stage + (wn * kGWaveN + i * 32) * kGK : stage + kGHalf + (wm * kGWaveM + (i - 4) * 32) * kGK;
+__device__ __forceinline__ const uint8_t* a_frag(const uint8_t* stage, int nf, int wn) {
+  return stage + (wn * kGWaveN + nf * 16) * kGK;
+}
+__device__ __forceinline__ const uint8_t* b_frag(const uint8_t* stage, int mf, int wm) {
+  return stage + kGHalf + (wm * kGWaveM + mf * 16) * kGK;
 }
 
-// One 32-byte k step of the wave's 128 x 64 sub-tile: 8 MFMAs on the fragments in `cur`,
-// interleaved with the reads of the next step's fragments into `nxt` and, in the step that
-// follows the barrier, the copies that refill the stage just consumed.
-template <bool kCopy>
-__device__ __forceinline__ void gemm_step(i32x16 (&acc)[4][kGMT], const i32x4 (&cur)[kGFrags],
-                                          i32x4 (&nxt)[kGFrags], const uint8_t* src, int off, int wn, int wm,
-                                          const int8_t* abase, const int8_t* bbase,
-                                          const uint32_t (&aoff)[kGCopies], const uint32_t (&boff)[kGCopies],
-                                          uint8_t* dst) {
+// One 64-byte k step of the wave's 128 x 64 sub-tile: 8 groups of 4 MFMAs, group nf on the
+// channel fragment in ring[nf % 4] and the 4 token fragments in b_cur.  Group nf reads the
+// channel fragment of group nf + 3 (of this step, or the next step's first three from
+// `a_next` at offset `off_next`) and, when b_from <= nf < b_from + 4, one token fragment of
+// the next step into b_nxt.
+template <int kBFrom>
+__device__ __forceinline__ void gemm_step(i32x4 (&acc)[kGNF][kGMF], i32x4 (&ring)[kGRing], const i32x4 (&b_cur)[kGMF],
+                                          i32x4 (&b_nxt)[kGMF], const uint8_t* a_src, int off, const uint8_t* a_next,
+                                          const uint8_t* b_next, int off_next, int wn, int wm) {
 #pragma unroll
-  for (int nt = 0; nt < 4; ++nt) {
-    nxt[nt] = *reinterpret_cast<const i32x4*>(frag_base(src, nt, wn, wm) + off);
-    if (nt < kGMT) nxt[4 + nt] = *reinterpret_cast<const i32x4*>(frag_base(src, 4 + nt, wn, wm) + off);
-    if constexpr (kCopy) {
-      flk::dma16_at(abase, aoff[nt], dst + nt * 8 * kGK);
-      flk::dma16_at(bbase, boff[nt], dst + kGHalf + nt * 8 * kGK);
-    }
+  for (int nf = 0; nf < kGNF; ++nf) {
 #pragma unroll
-    for (int mt = 0; mt < kGMT; ++mt)
-      acc[nt][mt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(cur[nt], cur[4 + mt], acc[nt][mt], 0, 0, 0);
+    for (int mf = 0; mf < kGMF; ++mf)
+      acc[nf][mf] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ring[nf % kGRing], b_cur[mf], acc[nf][mf], 0, 0, 0);
+    const int nl = nf + kGLead;
+    if (nl < kGNF) ring[nl % kGRing] = *reinterpret_cast<const i32x4*>(a_frag(a_src, nl, wn) + off);
+    else ring[nl % kGRing] = *reinterpret_cast<const i32x4*>(a_frag(a_next, nl - kGNF, wn) + off_next);
+    if (nf >= kBFrom && nf < kBFrom + kGMF)
+      b_nxt[nf - kBFrom] = *reinterpret_cast<const i32x4*>(b_frag(b_next, nf - kBFrom, wm) + off_next);
     __builtin_amdgcn_sched_barrier(0);
   }
 }
@@ -510,22 +521,24 @@ __global__ __launch_bounds__(kGThreads, 2) void w8a8_gemm_kernel(const GemmGroup
 
   const int KT = K / kGK;
   const int wn = wave >> 2, wm = wave & 3;     // 2 (channels) x 4 (tokens) waves
-  const int l32 = lane & 31, half = lane >> 5;
-  int off[4];
+  const int l16 = lane & 15, h4 = lane >> 4;
+  const int hperm = ((h4 & 1) << 1) | (h4 >> 1);
+  int off[2];   // fragment read offsets of k steps 0, 1: row l16, chunk 4 ks + perm(lane / 16)
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) off[ks] = l32 * kGK + (((2 * ks + half) ^ gswz(l32)) * 16);
+  for (int ks = 0; ks < 2; ++ks) off[ks] = l16 * kGK + (((4 * ks + hperm) ^ gswz(l16)) * 16);
 
-  i32x16 acc[4][kGMT];
+  i32x4 acc[kGNF][kGMF];
 #pragma unroll
-  for (int a = 0; a < 4; ++a)
+  for (int a = 0; a < kGNF; ++a)
 #pragma unroll
-    for (int b = 0; b < kGMT; ++b) acc[a][b] = i32x16{};
+    for (int b = 0; b < kGMF; ++b) acc[a][b] = i32x4{};
 
-  // Two stages.  Iteration kt multiplies k steps 0..2 of stage kt while reading the next
-  // step's fragments; then, once stage kt+1 has landed everywhere and every wave has read
-  // all of stage kt (the barrier), step 3 refills stage kt's buffer with stage kt+2 and
-  // reads step 0 of stage kt+1.  Past the last stage the copies repeat it (into the buffer
-  // no later step reads), so every iteration issues the same copies and vmcnt(0) is exact.
+  // Two stages of 128 k bytes, two 64-byte k steps each.  Stage kt: step 0 reads step 1's
+  // fragments as it goes; step 1 reads its own last channel fragments in groups 0-4, then --
+  // every wave done reading stage kt, stage kt+1 landed everywhere (the barrier) -- refills
+  // stage kt's buffer with stage kt+2 and reads stage kt+1's first fragments in groups 5-7.
+  // Past the last stage the copies repeat it (into the buffer no later step reads), so
+  // every stage issues the same copies and vmcnt(0) is exact.
   const int k1 = min(1, KT - 1) * kGK;
 #pragma unroll
   for (int i = 0; i < kGCopies; ++i) {
@@ -539,69 +552,103 @@ __global__ __launch_bounds__(kGThreads, 2) void w8a8_gemm_kernel(const GemmGroup
   }
   asm volatile("s_waitcnt vmcnt(%0)" :: "n"(2 * kGCopies) : "memory");   // stage 0 landed
   __syncthreads();
-  i32x4 ra[kGFrags], rb[kGFrags];
+  i32x4 ring[kGRing], b0[kGMF], b1[kGMF];
 #pragma unroll
-  for (int i = 0; i < kGFrags; ++i) ra[i] = *reinterpret_cast<const i32x4*>(frag_base(smem, i, wn, wm) + off[0]);
+  for (int mf = 0; mf < kGMF; ++mf) b0[mf] = *reinterpret_cast<const i32x4*>(b_frag(smem, mf, wm) + off[0]);
+#pragma unroll
+  for (int nf = 0; nf < kGLead; ++nf) ring[nf] = *reinterpret_cast<const i32x4*>(a_frag(smem, nf, wn) + off[0]);
+
+  auto mfma_group = [&](int nf, const i32x4 (&b)[kGMF]) {
+#pragma unroll
+    for (int mf = 0; mf < kGMF; ++mf)
+      acc[nf][mf] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ring[nf % kGRing], b[mf], acc[nf][mf], 0, 0, 0);
+  };
+  auto afrag = [&](const uint8_t* st, int nf, int o) { return *reinterpret_cast<const i32x4*>(a_frag(st, nf, wn) + o); };
+  auto bfrag = [&](const uint8_t* st, int mf, int o) { return *reinterpret_cast<const i32x4*>(b_frag(st, mf, wm) + o); };
 
   for (int kt = 0; kt < KT; ++kt) {
-    const int cur = (kt & 1) * kGStage, nxt = ((kt + 1) & 1) * kGStage;
+    const uint8_t* cs = smem + (kt & 1) * kGStage;          // stage kt
+    const uint8_t* ns = smem + ((kt + 1) & 1) * kGStage;    // stage kt+1
     const int k_next = min(kt + 2, KT - 1) * kGK;
-    gemm_step<false>(acc, ra, rb, smem + cur, off[1], wn, wm, abase, bbase, aoff, boff, nullptr);
-    gemm_step<false>(acc, rb, ra, smem + cur, off[2], wn, wm, abase, bbase, aoff, boff, nullptr);
-    gemm_step<false>(acc, ra, rb, smem + cur, off[3], wn, wm, abase, bbase, aoff, boff, nullptr);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // stage kt+1 landed
-    __syncthreads();
-    gemm_step<true>(acc, rb, ra, smem + nxt, off[0], wn, wm, abase + k_next, bbase + k_next, aoff, boff,
-                    wave_lds + cur);
+    // step 0
+#pragma unroll
+    for (int nf = 0; nf < kGNF; ++nf) {
+      mfma_group(nf, b0);
+      const int nl = nf + kGLead;
+      ring[nl % kGRing] = nl < kGNF ? afrag(cs, nl, off[0]) : afrag(cs, nl - kGNF, off[1]);
+      if (nf < kGMF) b1[nf] = bfrag(cs, nf, off[1]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // step 1, groups reading stage kt
+#pragma unroll
+    for (int nf = 0; nf < kGNF - kGLead; ++nf) {
+      mfma_group(nf, b1);
+      ring[(nf + kGLead) % kGRing] = afrag(cs, nf + kGLead, off[1]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");   // stage kt read, kt+1 landed
+#pragma unroll
+    for (int i = 0; i < kGCopies; ++i) {
+      flk::dma16_at(abase + k_next, aoff[i], wave_lds + (kt & 1) * kGStage + i * 8 * kGK);
+      flk::dma16_at(bbase + k_next, boff[i], wave_lds + (kt & 1) * kGStage + kGHalf + i * 8 * kGK);
+    }
+    // step 1, groups reading stage kt+1 (its step 0 fragments)
+#pragma unroll
+    for (int nf = kGNF - kGLead; nf < kGNF; ++nf) {
+      mfma_group(nf, b1);
+      ring[(nf + kGLead) % kGRing] = afrag(ns, nf + kGLead - kGNF, off[0]);
+      const int j = nf - (kGNF - kGLead);           // 0, 1, 2: token fragments 0-1, 2, 3
+      if (j == 0) {
+        b0[0] = bfrag(ns, 0, off[0]);
+        b0[1] = bfrag(ns, 1, off[0]);
+      } else {
+        b0[j + 1] = bfrag(ns, j + 1, off[0]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   if constexpr (kAcc) {
-    // Exact int32 products, straight from the accumulators.
+    // Exact int32 products, straight from the accumulators: the lane owns token l16 and
+    // channels 4 * (lane / 16) .. +3 of each 16 x 16 fragment.
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt)
+    for (int nf = 0; nf < kGNF; ++nf) {
+      const int n = n0 + wn * kGWaveN + nf * 16 + h4 * 4;
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int n = n0 + wn * kGWaveN + nt * 32 + g * 8 + half * 4;
-#pragma unroll
-        for (int mt = 0; mt < kGMT; ++mt) {
-          const int m = m0 + wm * kGWaveM + mt * 32 + l32;
-          if (n < N && m < M)
-            *reinterpret_cast<i32x4*>(acc_out + (int64_t)m * N + n) =
-                i32x4{acc[nt][mt][4 * g], acc[nt][mt][4 * g + 1], acc[nt][mt][4 * g + 2], acc[nt][mt][4 * g + 3]};
-        }
+      for (int mf = 0; mf < kGMF; ++mf) {
+        const int m = m0 + wm * kGWaveM + mf * 16 + l16;
+        if (n < N && m < M) *reinterpret_cast<i32x4*>(acc_out + (int64_t)m * N + n) = acc[nf][mf];
       }
+    }
   }
 
-  // Epilogue.  The lane owns token m = mt*32 + l32 and, per register group g, channels
-  // n = nt*32 + 8g + 4*half .. +3 of the wave's 128 x 64 sub-tile.  Rescaled bf16 values go
-  // to this wave's 16 KiB of the (now idle) LDS as [m][n] rows of 256 B whose 16-byte chunks
-  // are XOR-swizzled by m & 15; then the wave reads back 4 rows per instruction (16 lanes x
-  // 16 B per row) and writes each row's 256 contiguous bytes with 16-byte stores.
-  float am[kGMT];
+  // Epilogue.  The lane owns token m = mf*16 + l16 and channels n = nf*16 + 4 h4 .. +3 of the
+  // wave's 128 x 64 sub-tile.  Rescaled bf16 values go to this wave's 16 KiB of the (now
+  // idle) LDS as [m][n] rows of 256 B whose 16-byte chunks are XOR-swizzled by m & 15; then
+  // the wave reads back 4 rows per instruction (16 lanes x 16 B per row) and writes each
+  // row's 256 contiguous bytes with 16-byte stores.
+  float am[kGMF];
 #pragma unroll
-  for (int mt = 0; mt < kGMT; ++mt) am[mt] = a_scale[min(m0 + wm * kGWaveM + mt * 32 + l32, M - 1)];
+  for (int mf = 0; mf < kGMF; ++mf) am[mf] = a_scale[min(m0 + wm * kGWaveM + mf * 16 + l16, M - 1)];
   __syncthreads();   // every wave is done reading the operand stages
   uint8_t* const out_lds = smem + wave * (kGWaveM * 256);
 #pragma unroll
-  for (int nt = 0; nt < 4; ++nt) {
+  for (int nf = 0; nf < kGNF; ++nf) {
+    // w_o of the lane's 4 channels (clamped at the edge; clamped values are never stored)
+    const f32x4 w4 = *reinterpret_cast<const f32x4*>(w_scale + min(n0 + wn * kGWaveN + nf * 16 + h4 * 4, N - 4));
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      // w_o of the lane's 4 channels (clamped at the edge; clamped values are never stored)
-      const f32x4 w4 = *reinterpret_cast<const f32x4*>(w_scale + min(n0 + wn * kGWaveN + nt * 32 + g * 8 + half * 4, N - 4));
-#pragma unroll
-      for (int mt = 0; mt < kGMT; ++mt) {
-        const int ml = mt * 32 + l32;
-        const float y0 = ((float)acc[nt][mt][4 * g + 0] * am[mt]) * w4.x;
-        const float y1 = ((float)acc[nt][mt][4 * g + 1] * am[mt]) * w4.y;
-        const float y2 = ((float)acc[nt][mt][4 * g + 2] * am[mt]) * w4.z;
-        const float y3 = ((float)acc[nt][mt][4 * g + 3] * am[mt]) * w4.w;
-        uint2 packed;
-        packed.x = flk::pack_bf16x2(y0, y1);
-        packed.y = flk::pack_bf16x2(y2, y3);
-        const int chunk = (nt * 4 + g) ^ (ml & 15);
-        *reinterpret_cast<uint2*>(out_lds + ml * 256 + chunk * 16 + half * 8) = packed;
-      }
+    for (int mf = 0; mf < kGMF; ++mf) {
+      const int ml = mf * 16 + l16;
+      const float y0 = ((float)acc[nf][mf][0] * am[mf]) * w4.x;
+      const float y1 = ((float)acc[nf][mf][1] * am[mf]) * w4.y;
+      const float y2 = ((float)acc[nf][mf][2] * am[mf]) * w4.z;
+      const float y3 = ((float)acc[nf][mf][3] * am[mf]) * w4.w;
+      uint2 packed;
+      packed.x = flk::pack_bf16x2(y0, y1);
+      packed.y = flk::pack_bf16x2(y2, y3);
+      const int chunk = (nf * 2 + (h4 >> 1)) ^ (ml & 15);
+      *reinterpret_cast<uint2*>(out_lds + ml * 256 + chunk * 16 + (h4 & 1) * 8) = packed;
     }
   }
   // Each wave reads back only what it wrote itself: its LDS writes complete in order before
