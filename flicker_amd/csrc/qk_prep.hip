@@ -87,7 +87,7 @@ __device__ __forceinline__ void store16(uint16_t* p, uint4 v) {
   }
 }
 
-template <bool kScaleF32, bool kGain, int kHeads, bool kIds>
+template <bool kScaleF32, bool kGain, int kHeads>
 __global__ __launch_bounds__(kThreads) void qk_prep_kernel(
     const uint16_t* __restrict__ qkv, int64_t batch_stride, int64_t row_stride, RopeSource rope,
     const void* __restrict__ q_scale, const void* __restrict__ k_scale, float q_gain,
@@ -95,18 +95,6 @@ __global__ __launch_bounds__(kThreads) void qk_prep_kernel(
     uint16_t* __restrict__ v_out, int64_t out_length, int64_t out_offset) {
   const int lane = threadIdx.x & (kLanesPerRow - 1);
   const int t = blockIdx.x * kTokensPerBlock + (threadIdx.x >> 4);
-  // With ids, the block's first kHeadDim/2 threads compute each pair's frequency (and axis)
-  // once, with the table kernels' code, for every token of the block.
-  __shared__ float pair_freq[kIds ? kHeadDim / 2 : 1];
-  __shared__ int pair_axis[kIds ? kHeadDim / 2 : 1];
-  if constexpr (kIds) {
-    if (threadIdx.x < kHeadDim / 2) {
-      int axis;
-      pair_freq[threadIdx.x] = flk::pair_omega(threadIdx.x, rope.ax, rope.theta, axis);
-      pair_axis[threadIdx.x] = axis;
-    }
-    __syncthreads();
-  }
   if (t >= length) return;  // whole 16-lane rows exit together, so DPP rows stay intact
   const int h0 = blockIdx.y * kHeads;
   const int b = blockIdx.z;
@@ -120,23 +108,8 @@ __global__ __launch_bounds__(kThreads) void qk_prep_kernel(
     rv[i] = load16(row + (int64_t)(2 * num_heads + h0 + i) * kHeadDim);
   }
   float c[8], s[8], qs[8], ks[8];
-  if constexpr (kIds) {
-    // lane l holds lane-table columns 8l .. 8l+7 = pairs 4l .. 4l+3:
-    // cos column 2p, 2p+1 = cos(angle_p); sin columns = -sin(angle_p), +sin(angle_p)
-    const float* pos = rope.ids + (int64_t)t * rope.ids_stride;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      float cj, sj;
-      flk::pair_cos_sin(pos[pair_axis[lane * 4 + j]], pair_freq[lane * 4 + j], cj, sj);
-      c[2 * j] = cj;
-      c[2 * j + 1] = cj;
-      s[2 * j] = -sj;
-      s[2 * j + 1] = sj;
-    }
-  } else {
-    flk::load_table8(rope.cos + (int64_t)t * rope.table_stride, lane, c);
-    flk::load_table8(rope.sin + (int64_t)t * rope.table_stride, lane, s);
-  }
+  flk::load_table8(rope.cos + (int64_t)t * rope.table_stride, lane, c);
+  flk::load_table8(rope.sin + (int64_t)t * rope.table_stride, lane, s);
   flk::load_scale8<kScaleF32>(q_scale, lane, qs);
   flk::load_scale8<kScaleF32>(k_scale, lane, ks);
 
@@ -147,6 +120,76 @@ __global__ __launch_bounds__(kThreads) void qk_prep_kernel(
     store16(q_out + o, flk::norm_rotate<kScaleF32, kGain>(rq[i], qs, c, s, q_gain));
     store16(k_out + o, flk::norm_rotate<kScaleF32, false>(rk[i], ks, c, s, 1.0f));
     store16(v_out + o, rv[i]);
+  }
+}
+
+// The ids form.  Each 16-lane group computes the cos / sin of its 4 pairs once and applies
+// them to kRounds rounds of kHeads heads of its token; the next round's loads are issued
+// before the current round's math, so each lane keeps two rounds in flight while the trig of
+// one token serves kRounds * kHeads heads.  The block's first 64 threads compute the
+// (token-independent) pair frequencies into LDS after the first loads are issued.
+template <bool kScaleF32, bool kGain, int kHeads, int kRounds>
+__global__ __launch_bounds__(kThreads) void qk_prep_ids_kernel(
+    const uint16_t* __restrict__ qkv, int64_t batch_stride, int64_t row_stride, RopeSource rope,
+    const void* __restrict__ q_scale, const void* __restrict__ k_scale, float q_gain,
+    int length, int num_heads, uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_out,
+    uint16_t* __restrict__ v_out, int64_t out_length, int64_t out_offset) {
+  constexpr int kPairs = kHeadDim / 2;
+  __shared__ float pair_freq[kPairs];
+  __shared__ int pair_axis[kPairs];
+  const int lane = threadIdx.x & (kLanesPerRow - 1);
+  const int t = blockIdx.x * kTokensPerBlock + (threadIdx.x >> 4);
+  const int h0 = blockIdx.y * kHeads * kRounds;
+  const int b = blockIdx.z;
+  const bool live = t < length;
+  const uint16_t* row = qkv + (int64_t)b * batch_stride + (int64_t)t * row_stride + lane * 8;
+
+  uint4 buf[2][3 * kHeads];
+  auto load_round = [&](int r, uint4 (&dst)[3 * kHeads]) {
+#pragma unroll
+    for (int i = 0; i < kHeads; ++i) {
+      const int h = h0 + r * kHeads + i;
+      dst[3 * i] = load16(row + (int64_t)h * kHeadDim);
+      dst[3 * i + 1] = load16(row + (int64_t)(num_heads + h) * kHeadDim);
+      dst[3 * i + 2] = load16(row + (int64_t)(2 * num_heads + h) * kHeadDim);
+    }
+  };
+  if (live) load_round(0, buf[0]);
+  if (threadIdx.x < kPairs) {
+    int axis;
+    pair_freq[threadIdx.x] = flk::pair_omega(threadIdx.x, rope.ax, rope.theta, axis);
+    pair_axis[threadIdx.x] = axis;
+  }
+  __syncthreads();
+  if (!live) return;   // whole 16-lane rows exit together, so DPP rows stay intact
+
+  // lane l holds lane-table columns 8l .. 8l+7 = pairs 4l .. 4l+3:
+  // cos column 2p, 2p+1 = cos(angle_p); sin columns = -sin(angle_p), +sin(angle_p)
+  float c[8], s[8], qs[8], ks[8];
+  const float* pos = rope.ids + (int64_t)t * rope.ids_stride;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    float cj, sj;
+    flk::pair_cos_sin(pos[pair_axis[lane * 4 + j]], pair_freq[lane * 4 + j], cj, sj);
+    c[2 * j] = cj;
+    c[2 * j + 1] = cj;
+    s[2 * j] = -sj;
+    s[2 * j + 1] = sj;
+  }
+  flk::load_scale8<kScaleF32>(q_scale, lane, qs);
+  flk::load_scale8<kScaleF32>(k_scale, lane, ks);
+#pragma unroll
+  for (int r = 0; r < kRounds; ++r) {
+    if (r + 1 < kRounds) load_round(r + 1, buf[(r + 1) & 1]);
+    const uint4 (&cur)[3 * kHeads] = buf[r & 1];
+#pragma unroll
+    for (int i = 0; i < kHeads; ++i) {
+      const int h = h0 + r * kHeads + i;
+      const int64_t o = (((int64_t)b * num_heads + h) * out_length + out_offset + t) * kHeadDim + lane * 8;
+      store16(q_out + o, flk::norm_rotate<kScaleF32, kGain>(cur[3 * i], qs, c, s, q_gain));
+      store16(k_out + o, flk::norm_rotate<kScaleF32, false>(cur[3 * i + 1], ks, c, s, 1.0f));
+      store16(v_out + o, cur[3 * i + 2]);
+    }
   }
 }
 
@@ -162,20 +205,38 @@ struct Launch {
   int64_t out_length, out_offset;
 };
 
+#ifndef FLK_QK_IDS_ROUNDS
+#define FLK_QK_IDS_ROUNDS 3
+#endif
+
 template <bool kScaleF32, bool kGain, bool kIds>
 void launch(int heads_per_group, dim3 grid, hipStream_t stream, const Launch& a) {
-#define FLK_QK_LAUNCH(NH)                                                                       \
-  hipLaunchKernelGGL((qk_prep_kernel<kScaleF32, kGain, NH, kIds>), grid, dim3(kThreads), 0,     \
-                     stream, a.qkv, a.batch_stride, a.row_stride, a.rope, a.q_scale, a.k_scale, \
-                     a.q_gain, a.length, a.num_heads, a.q, a.k, a.v, a.out_length, a.out_offset)
-  switch (heads_per_group) {
-    case 6: FLK_QK_LAUNCH(6); break;
-    case 4: FLK_QK_LAUNCH(4); break;
-    case 3: FLK_QK_LAUNCH(3); break;
-    case 2: FLK_QK_LAUNCH(2); break;
-    default: FLK_QK_LAUNCH(1); break;
+#define FLK_QK_ARGS                                                                                \
+  a.qkv, a.batch_stride, a.row_stride, a.rope, a.q_scale, a.k_scale, a.q_gain, a.length, a.num_heads, \
+      a.q, a.k, a.v, a.out_length, a.out_offset
+#define FLK_QK_LAUNCH(NH) \
+  hipLaunchKernelGGL((qk_prep_kernel<kScaleF32, kGain, NH>), grid, dim3(kThreads), 0, stream, FLK_QK_ARGS)
+#define FLK_QK_IDS(NH, R) \
+  hipLaunchKernelGGL((qk_prep_ids_kernel<kScaleF32, kGain, NH, R>), grid, dim3(kThreads), 0, stream, FLK_QK_ARGS)
+  if constexpr (kIds) {
+    // heads_per_group = heads per round x rounds
+    if (heads_per_group % (2 * FLK_QK_IDS_ROUNDS) == 0 && heads_per_group == 2 * FLK_QK_IDS_ROUNDS)
+      FLK_QK_IDS(2, FLK_QK_IDS_ROUNDS);
+    else if (heads_per_group == 2) FLK_QK_IDS(2, 1);
+    else if (heads_per_group == 3) FLK_QK_IDS(3, 1);
+    else FLK_QK_IDS(1, 1);
+  } else {
+    switch (heads_per_group) {
+      case 6: FLK_QK_LAUNCH(6); break;
+      case 4: FLK_QK_LAUNCH(4); break;
+      case 3: FLK_QK_LAUNCH(3); break;
+      case 2: FLK_QK_LAUNCH(2); break;
+      default: FLK_QK_LAUNCH(1); break;
+    }
   }
+#undef FLK_QK_IDS
 #undef FLK_QK_LAUNCH
+#undef FLK_QK_ARGS
 }
 
 // Checks shared by both entry points: FLK_OK = launch, kEmpty = nothing to do (an empty
@@ -218,11 +279,10 @@ int dispatch(int hpg, int batch, int scale_is_f32, hipStream_t stream, const Lau
 
 // Heads per 16-lane group.  With tables, two measured best at the Klein shapes (6 loads in
 // flight per lane and 2x more blocks than four heads per group).  With ids, each group
-// computes 4 cos/sin pairs per token, which more heads share: measured at 1024^2, six heads
-// 33.3 us, three 33.4, four 33.8, two 35.9.
+// computes 4 cos/sin pairs per token, which more heads share.
 int heads_per_group(int num_heads, bool ids, int forced) {
   int hpg = (num_heads % 2 == 0) ? 2 : (num_heads % 3 == 0) ? 3 : 1;
-  if (ids) hpg = (num_heads % 6 == 0) ? 6 : (num_heads % 4 == 0) ? 4 : (num_heads % 3 == 0) ? 3 : hpg;
+  if (ids && num_heads % (2 * FLK_QK_IDS_ROUNDS) == 0) hpg = 2 * FLK_QK_IDS_ROUNDS;
   if (forced > 0 && num_heads % forced == 0) hpg = forced;
   return hpg;
 }
