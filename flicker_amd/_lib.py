@@ -29,6 +29,8 @@ SIGNATURES = {
     "flk_attend_to": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _i64, _i64, _i64, _p]),
     "flk_attend_split_to": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _i64, _i64, _i64, _i, _p, _i64, _p]),
     "flk_attend_split_static_to": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _i64, _i64, _i64, _i, _p]),
+    "flk_attend_balanced_to": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _i64, _i64, _i64, _p, _i64, _p]),
+    "flk_attend_balanced_plan": (_i, [_i, _i, _i, _ip, ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int64)]),
     "flk_attend_plan": (_i, [_i, _i, _i, _ip, ctypes.POINTER(ctypes.c_int64)]),
     "flk_rope_embed": (_i, [_p, _i64, _i64, _i, _ip, _f, _p, _p]),
     "flk_lane_pair": (_i, [_p, _i64, _i, _p, _p, _p]),
@@ -135,6 +137,37 @@ def attend_plan(batch: int, heads: int, length: int) -> tuple[int, int]:
     check(lib().flk_attend_plan(batch, heads, length, ctypes.byref(splits), ctypes.byref(nbytes)),
           "flk_attend_plan")
     return splits.value, nbytes.value
+
+
+@functools.lru_cache(maxsize=1024)
+def attend_balanced_plan(batch: int, heads: int, length: int) -> tuple[int, int, int]:
+    """(grid, workspace bytes, counters offset) of flk_attend_balanced_to for a shape; grid 0
+    when the shape has fewer 256-query tiles than CUs (a pure function of the shape)."""
+    grid, nbytes, off = ctypes.c_int(0), ctypes.c_int64(0), ctypes.c_int64(0)
+    check(lib().flk_attend_balanced_plan(batch, heads, length, ctypes.byref(grid), ctypes.byref(nbytes),
+                                         ctypes.byref(off)), "flk_attend_balanced_plan")
+    return grid.value, nbytes.value, off.value
+
+
+_BALANCED_WORKSPACE: dict = {}
+
+
+def balanced_workspace(device: torch.device, stream: int, nbytes: int, counters_offset: int) -> torch.Tensor:
+    """The balanced attend's workspace for one (device, stream): allocated zeroed on first use
+    and kept, since every call leaves its counters zero.  One per stream, so that calls on
+    different streams never share one.  Under graph capture a fresh workspace is taken from
+    the capture's pool and its counters are cleared by a captured fill, which every replay
+    repeats."""
+    if torch.cuda.is_current_stream_capturing():
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
+        ws[counters_offset:].zero_()
+        return ws
+    key = (device.index, stream)
+    ws = _BALANCED_WORKSPACE.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+        _BALANCED_WORKSPACE[key] = ws
+    return ws
 
 
 def int_array(values) -> ctypes.Array:

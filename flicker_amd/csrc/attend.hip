@@ -97,6 +97,7 @@ constexpr int kRowsPerWave = kBN / kWaves;     // tile rows each wave copies (8)
 constexpr int kDmaPerTensor = kRowsPerWave / 4;  // copy instructions per wave per tile (2)
 constexpr int kDmaPerIter = 2 * kDmaPerTensor;   // K and V
 constexpr int kXcds = 8;
+constexpr int kCUs = 256;                // MI355X compute units (one balanced block each)
 constexpr int kLead = 4;                 // slots between an operand's LDS read and its MFMA
 constexpr int kOpRing = 8;               // operand registers in flight (> kLead)
 // Slot n of every phase uses ops[n % kOpRing], and the next phase's first operands are read
@@ -273,33 +274,14 @@ __device__ __forceinline__ void iteration(WaveState& w, const Ctx& c, int t, int
   asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" :: "n"(kDmaPerIter) : "memory");
 }
 
-// kSplit = false: the block takes every key of its 256 queries and writes O.
-// kSplit = true: the key tiles are cut into `splits` ranges of equal length (+-1 tile); the
-// block takes one range and writes its unnormalised acc and l to part_acc / part_l, which
-// attend_merge_kernel sums.  Ring slots count from the block's first tile, so the unrolled
-// loop keeps literal ring positions wherever the range starts.  Without a
-// running max the partial sums of different key ranges add as they are.
-template <bool kSplit>
-__global__ __launch_bounds__(kThreads, 2) void attend_kernel(
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
-    const uint16_t* __restrict__ v, uint16_t* __restrict__ o, int length, int q_blocks,
-    int total_blocks, int heads, int splits, int64_t o_batch_stride, int64_t o_head_stride,
-    int64_t o_row_stride, float* __restrict__ part_acc, float* __restrict__ part_l) {
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[kSmemBytes];
-
-  // XCD-aware renumbering: hardware block id p runs on XCD p % 8; give each XCD a
-  // contiguous range of logical ids (head-major, then query tile, then key range), so the
-  // blocks that read one head's keys share an L2, and so do the key ranges of one query
-  // tile, whose partials attend_merge_kernel then reads on the same XCD.
-  const int p = blockIdx.x;
-  const int xcd = p % kXcds, local = p / kXcds;
-  const int per = total_blocks / kXcds, extra = total_blocks % kXcds;
-  const int logical = xcd * per + min(xcd, extra) + local;
-  const int split = kSplit ? logical % splits : 0;
-  const int rest = kSplit ? logical / splits : logical;
-  const int qblk = rest % q_blocks;
-  const int bh = rest / q_blocks;
-
+// One segment of work for a block: head bh (batch-major), query tile qblk, key tiles
+// [t_begin, t_end).  On return w holds the segment's unnormalised O^T accumulators and row
+// sums (lacc), and every LDS read and copy of the segment has completed.  Ring slots count from
+// the segment's first tile, so the unrolled loop keeps literal ring positions wherever the
+// range starts.
+__device__ __forceinline__ void attend_segment(WaveState& w, uint8_t* smem, const uint16_t* __restrict__ q,
+                                               const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+                                               int length, int bh, int qblk, int t_begin, int t_end) {
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   Ctx c;
@@ -309,11 +291,6 @@ __global__ __launch_bounds__(kThreads, 2) void attend_kernel(
   c.length = length;
   c.ntiles = (length + kBN - 1) / kBN;
   c.cp.last_tile = c.ntiles - 1;
-  int t_begin = 0, t_end = c.ntiles;   // this block's key tiles
-  if constexpr (kSplit) {
-    t_begin = split * c.ntiles / splits;
-    t_end = (split + 1) * c.ntiles / splits;
-  }
   c.cp.lds_wave_off = __builtin_amdgcn_readfirstlane(wave * kRowsPerWave * kRowBytes);
   {
     const int rows_last = length - c.cp.last_tile * kBN;   // 1..64 valid rows in the last tile
@@ -336,7 +313,6 @@ __global__ __launch_bounds__(kThreads, 2) void attend_kernel(
   for (int tl = 0; tl < 3; ++tl) copy_tile(smem + kKRing + tl * kTileBytes, c.kh, t_begin + tl, c.cp);
   for (int tl = 0; tl < 2; ++tl) copy_tile(smem + kVRing + tl * kTileBytes, c.vh, t_begin + tl, c.cp);
 
-  WaveState w;
   const int q0 = qblk * kBM + wave * 32;   // query group g of this wave: q0 + 16 g .. + 15
   // k-slots 8h..8h+7 of the S MFMAs take d chunk dperm = 4 st + perm(h) of the K and Q rows,
   // perm(h) = 0, 2, 1, 3: lanes l and l + 32 then read neighbouring chunks (c, c ^ 1), which
@@ -410,7 +386,7 @@ __global__ __launch_bounds__(kThreads, 2) void attend_kernel(
     iteration<false>(w, c, t + 3, 3);
   }
   for (; t < t_end; ++t) iteration<true>(w, c, t, (t - t_begin) & 3);
-  // No copy may still be writing this block's LDS when the block ends.
+  // No copy may still be writing this block's LDS when the segment ends.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   // Drain: O^T += V(U-1)^T P(U-1)^T for the last unit (unit 1 of the last tile).
@@ -427,41 +403,253 @@ __global__ __launch_bounds__(kThreads, 2) void attend_kernel(
     w.lacc[0] = mfma16(w.ones, pb0, w.lacc[0]);
     w.lacc[1] = mfma16(w.ones, pb1, w.lacc[1]);
   }
+}
 
-  // Epilogue: l of each query group from lanes 0-15 (row 0 of the row-sum tile) to the lanes
-  // of every lane group, O = bf16(acc / l), 4 d values per 8-byte store.
-  float l[2];
+// l of each query group from lanes 0-15 (row 0 of the row-sum tile) to the lanes of every
+// lane group.
+__device__ __forceinline__ void row_sums(const WaveState& w, float (&l)[2]) {
+  const int lane = threadIdx.x & 63;
 #pragma unroll
   for (int g = 0; g < 2; ++g) l[g] = __shfl(w.lacc[g][0], lane & 15);
-  if constexpr (kSplit) {
-    // Partials in the accumulator's own lane order, so each store is 64 lanes x 16 bytes
-    // contiguous: with unit = bh * q_blocks + qblk, register group i = 2 dt + g holds
-    // acc[d = 16 dt + 4h .. +3] of query q0 + 16 g + col at float4 index
-    //   ((split * units + unit) * 8 + wave) * 1024 + i * 64 + lane,
-    // and the l of wave query j (= 16 g + col) at ((split * units + unit) * 8 + wave) * 64 + j.
-    const int64_t units = total_blocks / splits;
-    const int64_t slot = ((int64_t)split * units + (int64_t)bh * q_blocks + qblk) * kWaves + wave;
-    f32x4* dst = reinterpret_cast<f32x4*>(part_acc) + slot * 1024 + lane;
+}
+
+// O = bf16(acc / l) of the wave's 32 queries, 4 d values per 8-byte store.
+__device__ __forceinline__ void store_o(const WaveState& w, const float (&l)[2], uint16_t* __restrict__ o, int bh,
+                                        int heads, int qblk, int length, int64_t o_batch_stride,
+                                        int64_t o_head_stride, int64_t o_row_stride) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int h4 = lane >> 4, col = lane & 15;
+  const int q0 = qblk * kBM + wave * 32;
+  const int b = bh / heads, hd = bh - b * heads;
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt)
+  for (int g = 0; g < 2; ++g) {
+    const int qi = q0 + g * 16 + col;
+    if (qi >= length) continue;
+    uint16_t* orow = o + b * o_batch_stride + hd * o_head_stride + (int64_t)qi * o_row_stride;
 #pragma unroll
-      for (int g = 0; g < 2; ++g) dst[(dt * 2 + g) * 64] = w.oacc[dt][g];
-    if (c.h < 2) part_l[slot * 64 + lane] = l[c.h];   // lanes 0-15: group 0, 16-31: group 1
-  } else {
-    const int b = bh / heads, hd = bh - b * heads;
+    for (int dt = 0; dt < 8; ++dt) {
+      const int d0 = dt * 16 + h4 * 4;
+      uint2 val;
+      val.x = flk::pack_bf16x2(w.oacc[dt][g][0] / l[g], w.oacc[dt][g][1] / l[g]);
+      val.y = flk::pack_bf16x2(w.oacc[dt][g][2] / l[g], w.oacc[dt][g][3] / l[g]);
+      *reinterpret_cast<uint2*>(orow + d0) = val;
+    }
+  }
+}
+
+// Partials of one 256-query tile in the accumulator's own lane order, so each store is 64
+// lanes x 16 bytes contiguous: register group i = 2 dt + g of wave w holds acc[d = 16 dt +
+// 4h .. +3] of query q0 + 16 g + col at float4 index (slot * 8 + w) * 1024 + i * 64 + lane,
+// and the l of wave query j (= 16 g + col) at (slot * 8 + w) * 64 + j.
+// kCoherent: every word is written by a relaxed device-scope atomic store (a store that
+// is coherent across the device on its own, so a reader on any CU that loads it the same
+// way after the writer's stores have completed sees it; no cache-wide write-back needed).
+template <bool kCoherent = false>
+__device__ __forceinline__ void store_partial(const WaveState& w, const float (&l)[2], float* __restrict__ part_acc,
+                                              float* __restrict__ part_l, int64_t slot) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t ws = slot * kWaves + wave;
+  f32x4* dst = reinterpret_cast<f32x4*>(part_acc) + ws * 1024 + lane;
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
     for (int g = 0; g < 2; ++g) {
-      const int qi = q0 + g * 16 + col;
-      if (qi >= length) continue;
-      uint16_t* orow = o + b * o_batch_stride + hd * o_head_stride + (int64_t)qi * o_row_stride;
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-        const int d0 = dt * 16 + c.h * 4;
-        uint2 val;
-        val.x = flk::pack_bf16x2(w.oacc[dt][g][0] / l[g], w.oacc[dt][g][1] / l[g]);
-        val.y = flk::pack_bf16x2(w.oacc[dt][g][2] / l[g], w.oacc[dt][g][3] / l[g]);
-        *reinterpret_cast<uint2*>(orow + d0) = val;
+      if constexpr (kCoherent) {
+        union { f32x4 f; uint64_t u[2]; } x;
+        x.f = w.oacc[dt][g];
+        uint64_t* d = reinterpret_cast<uint64_t*>(dst + (dt * 2 + g) * 64);
+        __hip_atomic_store(d, x.u[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(d + 1, x.u[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      } else {
+        dst[(dt * 2 + g) * 64] = w.oacc[dt][g];
       }
+    }
+  if ((lane >> 4) < 2) {   // lanes 0-15: group 0, 16-31: group 1
+    if constexpr (kCoherent)
+      __hip_atomic_store(part_l + ws * 64 + lane, l[lane >> 4], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else
+      part_l[ws * 64 + lane] = l[lane >> 4];
+  }
+}
+
+// Adds the partial that store_partial<true> wrote to `slot` into the wave's registers, with
+// relaxed device-scope atomic loads (coherent with those stores).
+__device__ __forceinline__ void add_partial(WaveState& w, float (&l)[2], const float* __restrict__ part_acc,
+                                            const float* __restrict__ part_l, int64_t slot) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t ws = slot * kWaves + wave;
+  const f32x4* src = reinterpret_cast<const f32x4*>(part_acc) + ws * 1024 + lane;
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      const uint64_t* s = reinterpret_cast<const uint64_t*>(src + (dt * 2 + g) * 64);
+      union { f32x4 f; uint64_t u[2]; } x;
+      x.u[0] = __hip_atomic_load(s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      x.u[1] = __hip_atomic_load(s + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      w.oacc[dt][g] += x.f;
+    }
+#pragma unroll
+  for (int g = 0; g < 2; ++g)
+    l[g] += __hip_atomic_load(part_l + ws * 64 + g * 16 + (lane & 15), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// kSplit = false: the block takes every key of its 256 queries and writes O.
+// kSplit = true: the key tiles are cut into `splits` ranges of equal length (+-1 tile); the
+// block takes one range and writes its unnormalised acc and l to part_acc / part_l, which
+// attend_merge_kernel sums.  Without a running max the partial sums of different key ranges
+// add as they are.
+template <bool kSplit>
+__global__ __launch_bounds__(kThreads, 2) void attend_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+    const uint16_t* __restrict__ v, uint16_t* __restrict__ o, int length, int q_blocks,
+    int total_blocks, int heads, int splits, int64_t o_batch_stride, int64_t o_head_stride,
+    int64_t o_row_stride, float* __restrict__ part_acc, float* __restrict__ part_l) {
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[kSmemBytes];
+
+  // XCD-aware renumbering: hardware block id p runs on XCD p % 8; give each XCD a
+  // contiguous range of logical ids (head-major, then query tile, then key range), so the
+  // blocks that read one head's keys share an L2, and so do the key ranges of one query
+  // tile, whose partials attend_merge_kernel then reads on the same XCD.
+  const int p = blockIdx.x;
+  const int xcd = p % kXcds, local = p / kXcds;
+  const int per = total_blocks / kXcds, extra = total_blocks % kXcds;
+  const int logical = xcd * per + min(xcd, extra) + local;
+  const int split = kSplit ? logical % splits : 0;
+  const int rest = kSplit ? logical / splits : logical;
+  const int qblk = rest % q_blocks;
+  const int bh = rest / q_blocks;
+  const int ntiles = (length + kBN - 1) / kBN;
+  int t_begin = 0, t_end = ntiles;   // this block's key tiles
+  if constexpr (kSplit) {
+    t_begin = split * ntiles / splits;
+    t_end = (split + 1) * ntiles / splits;
+  }
+
+  WaveState w;
+  attend_segment(w, smem, q, k, v, length, bh, qblk, t_begin, t_end);
+  float l[2];
+  row_sums(w, l);
+  if constexpr (kSplit) {
+    const int64_t units = total_blocks / splits;
+    store_partial(w, l, part_acc, part_l, (int64_t)split * units + (int64_t)bh * q_blocks + qblk);
+  } else {
+    store_o(w, l, o, bh, heads, qblk, length, o_batch_stride, o_head_stride, o_row_stride);
+  }
+}
+
+// Balanced attend: one persistent block per CU (256), so that the last, partial round of
+// tiles is shared by all the CUs.  Tiles (b, h, 256-query tile) are dealt to the 8 XCDs in
+// contiguous ranges (keeping each head's K/V in one L2).  On an XCD with n tiles and C = 32
+// CUs, CU l first takes tiles l, l + C, ... whole for R = floor(n / C) rounds -- the plain
+// kernel's rounds, every CU streaming the keys from tile 0 together, so that K/V tiles are
+// shared in the L2 as they arrive.  The r = n - R C tiles left over are cut by keys: CU l < r
+// takes the first f key tiles of leftover tile l, and the other h = C - r CUs ("helpers") take
+// the rest [f, ntiles) of the leftover tiles, helper j those with index = j mod h -- at most
+// m = ceil(r / h) each, with f chosen so that no helper outlasts the first parts, counting
+// each segment's fixed cost.  The last round then costs about f / ntiles of a tile instead
+// of a whole one (half a tile when the helpers outnumber the leftover tiles, m = 1).
+//
+// Each cut tile has exactly two pieces, which write their (acc, l) partials to its two slots
+// with coherent stores and, once those have completed, increment its counter; the piece that
+// finds the counter at 1 is second: it adds the other piece's partial to its own registers
+// (a + b = b + a, so the result does not depend on the order of arrival), writes O and resets
+// the counter to 0 for the next launch.  No block ever waits for another.  A device-scope
+// fence here would write back and invalidate the whole L2 of the XCD for every piece, which
+// stalls every block streaming keys through that L2 (tens of microseconds per fence).
+struct BalancedPlan {
+  int units, ntiles, grid;
+};
+
+// The leftover split of an XCD with n tiles: rounds R, leftover r, helpers h, first-part
+// length f (f == ntiles: the leftover tiles are not cut, each runs whole on CU l < r).
+// Fixed cost of one segment in key tiles: its prologue (Q and the first K/V tiles from
+// memory, ~4.5 us when every CU starts at once) plus the partial hand-off (~4 us), against
+// ~1.5 us per key tile (measured at 4608 keys).
+constexpr int kSegmentTiles = 6;
+
+struct XcdSplit {
+  int ux0, R, r, h, f;
+};
+
+__device__ __forceinline__ XcdSplit xcd_split(const BalancedPlan& bp, int x) {
+  constexpr int C = kCUs / kXcds;
+  XcdSplit xs;
+  xs.ux0 = (int)((int64_t)x * bp.units / kXcds);
+  const int n = (int)((int64_t)(x + 1) * bp.units / kXcds) - xs.ux0;
+  xs.R = n / C;
+  xs.r = n - xs.R * C;
+  xs.h = C - xs.r;
+  const int m = xs.r > 0 ? (xs.r + xs.h - 1) / xs.h : 1;
+  // First part f + s against m second parts m (ntiles - f + s), s = a segment's fixed cost in
+  // key tiles: f = ceil((m ntiles + (m - 1) s) / (m + 1)), at most ntiles (then no cut).
+  xs.f = min(bp.ntiles, (m * bp.ntiles + (m - 1) * kSegmentTiles + m) / (m + 1));
+  return xs;
+}
+
+__global__ __launch_bounds__(kThreads, 2) void attend_balanced_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+    const uint16_t* __restrict__ v, uint16_t* __restrict__ o, int length, int q_blocks, int units,
+    int heads, int64_t o_batch_stride, int64_t o_head_stride, int64_t o_row_stride,
+    float* __restrict__ part_acc, float* __restrict__ part_l, int* __restrict__ counters) {
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[kSmemBytes];
+  __shared__ int arrival;
+  constexpr int C = kCUs / kXcds;
+  const int x = blockIdx.x % kXcds, l = blockIdx.x / kXcds;   // hardware deals blocks round-robin over XCDs
+  const BalancedPlan bp{units, (length + kBN - 1) / kBN, (int)gridDim.x};
+  const XcdSplit xs = xcd_split(bp, x);
+
+  // This block's segments: R whole tiles, then its leftover pieces (one first part, or up to
+  // m second parts, or -- when the tiles are too short to cut -- one whole leftover tile).
+  const int left0 = xs.ux0 + xs.R * C;   // first leftover tile of this XCD
+  const bool cut = xs.f < bp.ntiles;
+  const int hh = l - xs.r;               // helper index (>= 0 for helpers)
+  int nleft = 0;
+  if (xs.r > 0) {
+    if (!cut || l < xs.r) nleft = l < xs.r ? 1 : 0;
+    else nleft = hh < xs.r ? (xs.r - 1 - hh) / xs.h + 1 : 0;
+  }
+  for (int sg = 0; sg < xs.R + nleft; ++sg) {
+    int unit, t0 = 0, t1 = bp.ntiles, slot = -1, piece = 0;
+    if (sg < xs.R) {
+      unit = xs.ux0 + sg * C + l;
+    } else if (!cut) {
+      unit = left0 + l;
+    } else if (l < xs.r) {
+      unit = left0 + l;
+      t1 = xs.f;
+      slot = x * C + l;
+    } else {
+      const int i = hh + (sg - xs.R) * xs.h;
+      unit = left0 + i;
+      t0 = xs.f;
+      slot = x * C + i;
+      piece = 1;
+    }
+    const int bh = unit / q_blocks, qblk = unit - bh * q_blocks;
+    __syncthreads();   // every wave is done with the previous segment's LDS
+    WaveState w;
+    attend_segment(w, smem, q, k, v, length, bh, qblk, t0, t1);
+    float ls[2];
+    row_sums(w, ls);
+    if (slot < 0) {
+      store_o(w, ls, o, bh, heads, qblk, length, o_batch_stride, o_head_stride, o_row_stride);
+      continue;
+    }
+    // Hand-off without a cache-wide fence: the partial goes out as coherent stores, the
+    // wave waits until they have completed (vmcnt counts them until the memory system has
+    // acknowledged them), the barrier then orders every wave's completed stores before the
+    // counter increment.  The second arriver's coherent loads issue only after its increment
+    // has returned 1, i.e. after both pieces' stores completed.
+    store_partial<true>(w, ls, part_acc, part_l, (int64_t)slot * 2 + piece);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0) arrival = atomicAdd(&counters[slot], 1);
+    __syncthreads();
+    if (arrival == 1) {   // second: add the other piece's partial, write O
+      add_partial(w, ls, part_acc, part_l, (int64_t)slot * 2 + (1 - piece));
+      store_o(w, ls, o, bh, heads, qblk, length, o_batch_stride, o_head_stride, o_row_stride);
+      if (threadIdx.x == 0) counters[slot] = 0;
     }
   }
 }
@@ -514,7 +702,6 @@ namespace {
 // Blocks per launch below which the key range is split: a grid this small leaves CUs idle
 // for the whole launch (256 CUs, one block each).
 constexpr int kSplitBelow = 192;
-constexpr int kCUs = 256;
 
 // Argument checks shared by the entry points: FLK_OK = launch, kNothing = empty input (nothing
 // to do), else an error status.
@@ -571,6 +758,64 @@ extern "C" int flk_attend_to(const void* q, const void* k, const void* v, void* 
                               o_row_stride);
   if (st != FLK_OK) return st == kNothing ? FLK_OK : st;
   return launch_attend(q, k, v, o, batch, heads, length, o_batch_stride, o_head_stride, o_row_stride, stream);
+}
+
+namespace {
+
+// Workspace of a balanced launch on `grid` blocks: two partial slots per cut tile, at most
+// one cut tile per block (acc: 8 waves x 1024 float4; l: 8 waves x 64 floats), then one int
+// counter per cut tile.
+constexpr int64_t kSlotAccBytes = (int64_t)kWaves * 1024 * 16;
+constexpr int64_t kSlotLBytes = (int64_t)kWaves * 64 * 4;
+
+int64_t balanced_counters_offset(int grid) { return 2 * (int64_t)grid * (kSlotAccBytes + kSlotLBytes); }
+int64_t balanced_workspace_bytes(int grid) { return balanced_counters_offset(grid) + 4 * (int64_t)grid; }
+
+// Whether the balanced launch beats one block per tile, by the tiles an XCD has left after
+// its full rounds of 32: it does when every XCD has at least one full round and the last
+// round would leave more than 3/8 of the CUs idle (measured: 11% at 64 or 88 of 256 CUs
+// busy, 7% at 48, 2.5% at 152), and not at 176 of 256 (a plain last round on fewer CUs runs
+// at a higher clock under the power limit, which makes up for the idle CUs, and cutting a
+// tile costs ~9 us per piece) nor with no full round (144 tiles: 47 us against 39 us).
+bool balanced_preferred(int batch, int heads, int length) {
+  const int64_t units = q_tiles(length) * batch * heads;
+  constexpr int C = kCUs / kXcds;
+  if (units < kCUs || units > INT32_MAX) return false;
+  const int64_t left = ((units + kXcds - 1) / kXcds) % C;   // leftover tiles of the fullest XCD
+  return left > 0 && left * 8 <= C * 5;
+}
+
+}  // namespace
+
+extern "C" int flk_attend_balanced_plan(int batch, int heads, int length, int* grid, int64_t* workspace_bytes,
+                                        int64_t* counters_offset) {
+  if (batch < 0 || heads < 0 || length < 0 || !grid || !workspace_bytes || !counters_offset) return FLK_E_INVALID;
+  *grid = balanced_preferred(batch, heads, length) ? kCUs : 0;
+  *workspace_bytes = balanced_workspace_bytes(kCUs);
+  *counters_offset = balanced_counters_offset(kCUs);
+  return FLK_OK;
+}
+
+extern "C" int flk_attend_balanced_to(const void* q, const void* k, const void* v, void* o, int batch, int heads,
+                                      int length, int head_dim, int64_t o_batch_stride, int64_t o_head_stride,
+                                      int64_t o_row_stride, void* workspace, int64_t workspace_bytes,
+                                      void* stream) {
+  const int st = check_attend(q, k, v, o, batch, heads, length, head_dim, o_batch_stride, o_head_stride,
+                              o_row_stride);
+  if (st != FLK_OK) return st == kNothing ? FLK_OK : st;
+  const int64_t units = q_tiles(length) * batch * heads;   // <= INT32_MAX (check_attend)
+  constexpr int grid = kCUs;
+  if (!workspace || workspace_bytes < balanced_workspace_bytes(grid)) return FLK_E_INVALID;
+  if (!flk_host_aligned(workspace, 16)) return FLK_E_ALIGN;
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  float* part_acc = reinterpret_cast<float*>(ws);
+  float* part_l = reinterpret_cast<float*>(ws + 2 * (int64_t)grid * kSlotAccBytes);
+  int* counters = reinterpret_cast<int*>(ws + balanced_counters_offset(grid));
+  hipLaunchKernelGGL(attend_balanced_kernel, dim3((unsigned)grid), dim3(kThreads), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
+                     static_cast<uint16_t*>(o), length, (int)q_tiles(length), (int)units, heads, o_batch_stride,
+                     o_head_stride, o_row_stride, part_acc, part_l, counters);
+  return flk_launch_status();
 }
 
 extern "C" int flk_attend_plan(int batch, int heads, int length, int* splits, int64_t* workspace_bytes) {

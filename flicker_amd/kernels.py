@@ -283,15 +283,29 @@ def attend_merged(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
     return out
 
 
-def _launch_attend(q, k, v, out, o_strides, splits: int | None) -> None:
-    """O through strides (batch, head, row); the key-split path when the grid is small."""
+def _launch_attend(q, k, v, out, o_strides, splits: int | None, balanced: bool | None = None) -> None:
+    """O through strides (batch, head, row): with ``splits`` None the plan's choice -- the
+    key-split path when the grid is small, the balanced path (flk_attend_balanced_to: one
+    persistent block per CU, the last round's tiles cut by keys) when flk_attend_balanced_plan
+    prefers it, else one block per tile.  An explicit ``splits`` forces that split count
+    (1 = one block per tile, flk_attend_to); ``balanced=True`` forces the balanced launch."""
     batch, heads, length, dim = q.shape
     planned, _ = _lib.attend_plan(batch, heads, length)
-    splits = planned if splits is None else int(splits)
     groups = max(1, -(-length // 256))
+    args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), batch, heads, length, dim, *o_strides)
+    if balanced is None:
+        balanced = splits is None and planned == 1 and _lib.attend_balanced_plan(batch, heads, length)[0] > 0
+    if balanced:
+        if splits not in (None, 1):
+            raise ValueError(f"the balanced launch takes no key split, got splits={splits}")
+        _, nbytes, counters = _lib.attend_balanced_plan(batch, heads, length)
+        stream = _lib.stream_of(q)
+        ws = _lib.balanced_workspace(q.device, stream, nbytes, counters)
+        _lib.run("flk_attend_balanced_to", (q, k, v, out, ws), *args, ws.data_ptr(), nbytes, stream)
+        return
+    splits = planned if splits is None else int(splits)
     if not 1 <= splits <= groups:
         raise ValueError(f"splits must be in [1, {groups}] for L={length}, got {splits}")
-    args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), batch, heads, length, dim, *o_strides)
     if splits == 1:
         _lib.run("flk_attend_to", (q, k, v, out), *args, _lib.stream_of(q))
         return

@@ -144,6 +144,40 @@ int flk_attend_split_static_to(const void* q, const void* k, const void* v, void
                                int splits, void* stream);
 
 /*
+ * flk_attend_to with the work spread evenly over the GPU's 256 CUs.  The same attend
+ * (src/flicker/kernels.py:105-145): instead of one block per (b, h, 256-query tile) -- 432
+ * tiles at the Klein 1024^2 shape, 1.69 rounds of 256 CUs -- 256 persistent blocks, 32 per
+ * XCD.  Each XCD takes a contiguous range of tiles; its CUs do whole tiles for as many full
+ * rounds as the range holds, and the tiles left over are cut by keys into two pieces: a
+ * first part of f key tiles on one CU and the rest on one of the CUs that had no leftover
+ * tile, f chosen so that no CU does more than f.  The two pieces' (acc, l) partials are
+ * added by whichever finishes second (plain sums: the reference keeps no running max); no
+ * block waits for another.  Only the f32 summation order of the cut tiles differs from
+ * flk_attend_to; the results are deterministic for a given shape.
+ *   - Takes every shape flk_attend_to takes; flk_attend_balanced_plan says whether it is the
+ *     faster launch for a shape.
+ *   - `workspace`: caller-owned, 16-byte aligned, at least flk_attend_balanced_plan's bytes.
+ *     The int counters at its counters_offset must be zero before the first call that uses
+ *     it (allocate it zeroed); each call leaves them zero.  Calls that share one workspace
+ *     must not overlap (one workspace per stream).
+ *   - Other arguments as flk_attend_to.
+ */
+int flk_attend_balanced_to(const void* q, const void* k, const void* v, void* o,
+                           int batch, int heads, int length, int head_dim,
+                           int64_t o_batch_stride, int64_t o_head_stride, int64_t o_row_stride,
+                           void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * Whether flk_attend_balanced_to is the faster launch for a shape (*grid = its block count,
+ * 256, else 0: with fewer than 256 tiles, or a last round of tiles filling more than 5/8 of
+ * the CUs, one block per tile -- or the key split -- is as fast or faster), its workspace
+ * size and the byte offset of the counters that must start at zero (both independent of the
+ * shape).  No device work.
+ */
+int flk_attend_balanced_plan(int batch, int heads, int length, int* grid, int64_t* workspace_bytes,
+                             int64_t* counters_offset);
+
+/*
  * The split count flk_attend_split_to should use for a shape, and its workspace size.
  * *splits = 1 (workspace 0) when the plain grid already has >= 192 blocks of 256 queries.
  * Otherwise it takes as many ranges as fill the 256 CUs once, keeping at least 512 keys per

@@ -1,0 +1,120 @@
+"""The balanced attend (flk_attend_balanced_to: one persistent block per CU; each XCD's tiles
+left over after its full rounds cut by keys into two pieces, merged by whichever piece
+finishes second) against the bounded oracle and against the one-block-per-tile kernel.
+
+Gates: the tight bounded-oracle gate of test_gpu_attend; against flk_attend_to only the cut
+tiles may differ, by the f32 order of two partial sums (at most one bf16 ulp of the largest
+output); every output element is written (a NaN sentinel survives nowhere); repeated calls
+are bit-identical (the merge order does not depend on which piece arrives first) and leave
+the workspace counters at zero; a captured graph replays to the eager result."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from flicker_amd import _lib, kernels
+from oracle import path as P
+from tests._util import to_np
+from tests.test_gpu_attend import prepped_case, tight_gate
+
+pytestmark = pytest.mark.gpu
+D = 128
+
+
+def run(q, k, v, splits=None, balanced=True):
+    out = torch.full_like(q, float("nan"))
+    kernels._launch_attend(q, k, v, out, out.stride()[:3], splits, balanced)
+    torch.cuda.synchronize()
+    return out
+
+
+def counters_zero(q):
+    batch, heads, length, _ = q.shape
+    _, nbytes, off = _lib.attend_balanced_plan(batch, heads, length)
+    ws = _lib._BALANCED_WORKSPACE[(q.device.index, _lib.stream_of(q))]
+    return bool((ws[off:nbytes] == 0).all())
+
+
+@pytest.mark.parametrize("batch,heads,length", [(1, 128, 512), (1, 64, 1000), (2, 32, 1024), (1, 5, 1536),
+                                                 (1, 9, 4352), (1, 40, 1000)])
+def test_balanced_matches_oracle(device, batch, heads, length):
+    """Exactly 256 (b, h, 256-query tile) units: no cut (L = 1000: a masked last key tile);
+    30 units (fewer than the XCDs' CUs: every tile of an XCD cut); 153 units at 68 key tiles
+    (first part + one or two second parts per helper); 160 units at L = 1000 (cut tiles
+    with a masked last key tile in the second piece)."""
+    print(f"balanced B={batch} H={heads} L={length}", flush=True)
+    q, k, v = prepped_case(batch, heads, length, seed=length + heads)
+    qd, kd, vd = (t.to(device) for t in (q, k, v))
+    got = run(qd, kd, vd)
+    assert not torch.isnan(got).any(), "an output tile was never written"
+    want = P.attend_bounded(to_np(q), to_np(k), to_np(v))
+    tight_gate(f"balanced B{batch} H{heads} L{length}", to_np(got), want.astype(np.float64))
+    plain = run(qd, kd, vd, splits=1, balanced=False)
+    diff = (got.float() - plain.float()).abs()
+    scale = float(plain.float().abs().max())
+    assert float(diff.max()) <= 2.0 ** (math.floor(math.log2(scale)) - 7), float(diff.max())
+    assert counters_zero(qd)
+
+
+def test_balanced_klein_1024_deterministic(device):
+    """The headline shape (432 tiles): bit-identical over repeated calls, every element written,
+    within one ulp of the one-block-per-tile kernel, and the counters back at zero."""
+    from flicker_amd import workloads
+    w = workloads.WORKLOADS["klein_1024"]
+    q, k, v = (t.to(device) for t in prepped_case(1, w.num_heads, w.length, seed=3))
+    first = run(q, k, v)
+    assert not torch.isnan(first).any()
+    for i in range(10):
+        again = run(q, k, v)
+        assert torch.equal(first, again), f"call {i} differs"
+    assert counters_zero(q)
+    plain = run(q, k, v, splits=1, balanced=False)
+    diff = (first.float() - plain.float()).abs()
+    scale = float(plain.float().abs().max())
+    assert float(diff.max()) <= 2.0 ** (math.floor(math.log2(scale)) - 7)
+    print(f"klein_1024 balanced vs plain: mismatch {float((diff > 0).float().mean()):.3g}")
+    # sampled rows of two heads against the oracle
+    heads_sel, rows = [3, 17], np.linspace(0, w.length - 1, 256).astype(int)
+    qs, ks, vs = (to_np(t)[:, heads_sel] for t in (q, k, v))
+    want = P.attend_bounded(qs, ks, vs)[:, :, rows]
+    tight_gate("klein_1024 sampled", to_np(first)[:, heads_sel][:, :, rows], want.astype(np.float64))
+
+
+def test_balanced_graph_replay(device):
+    """Captured on a side stream (workspace from the capture's pool, counters cleared by a
+    captured fill), replayed three times with eager balanced calls between replays; 160
+    tiles, so every tile is cut and merged through the counters."""
+    heads, length = 40, 1024
+    g = torch.Generator().manual_seed(9)
+
+    def fresh():
+        x = torch.randn(3, 1, heads, length, D, generator=g)
+        x[:2] /= x[:2].pow(2).mean(-1, keepdim=True).sqrt()
+        x[0] /= math.sqrt(D)
+        return tuple(t.to(torch.bfloat16).to(device) for t in x)
+
+    static = fresh()
+    static_o = torch.empty_like(static[0])
+    def attend(q, k, v, out=None):
+        out = torch.empty_like(q) if out is None else out
+        kernels._launch_attend(q, k, v, out, out.stride()[:3], None, True)
+        return out
+
+    attend(*static, out=static_o)      # warm-up outside the capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        attend(*static, out=static_o)
+    for _ in range(3):
+        new = fresh()
+        for s, n in zip(static, new):
+            s.copy_(n)
+        graph.replay()
+        eager = attend(*fresh())         # eager balanced work between replays
+        torch.cuda.synchronize()
+        want = attend(*new)
+        torch.cuda.synchronize()
+        assert torch.equal(static_o, want)
+        assert eager.shape == want.shape

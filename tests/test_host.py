@@ -100,6 +100,35 @@ def test_attend_split_plan_and_validation(lib):
                    "flk_attend_plan")
 
 
+def test_attend_balanced_plan_and_validation(lib):
+    """flk_attend_balanced_plan prefers the balanced launch only where every XCD has a full
+    round of 32 tiles and the fullest XCD's last round would be at most 5/8 full (Klein
+    1024^2: 54 tiles per XCD, 22 left over -> one block per tile; 2048^2: 198 -> 6 left over
+    -> balanced; 512^2: 18 -> one block per tile); its workspace does not depend on the
+    shape.  flk_attend_balanced_to rejects short or misaligned workspaces before launching
+    anything."""
+    ws = 2 * 256 * (8 * 1024 * 16 + 8 * 64 * 4)
+    cases = {(1, 24, 4608): 0, (4, 24, 4608): 0, (1, 24, 16896): 256, (1, 24, 4352): 256, (1, 32, 4608): 256,
+             (1, 24, 6400): 256, (1, 128, 512): 0, (1, 6, 4608): 0, (1, 24, 1536): 0, (1, 40, 1000): 0,
+             (0, 3, 4608): 0}
+    for (b, h, length), want in cases.items():
+        grid, nbytes, counters = _lib.attend_balanced_plan(b, h, length)
+        assert grid == want, (b, h, length, grid)
+        assert (nbytes, counters) == (ws + 4 * 256, ws)
+    f = lib.flk_attend_balanced_to
+    hd = 24 * 128
+    args = (FAKE, FAKE, FAKE, FAKE, 1, 24, 4608, 128, 4608 * hd, 128, hd)
+    assert f(*args, FAKE, ws + 4 * 256 - 1, None) == _lib.FLK_E_INVALID
+    assert f(*args, None, ws + 4 * 256, None) == _lib.FLK_E_INVALID
+    assert f(*args, FAKE + 8, ws + 4 * 256, None) == _lib.FLK_E_ALIGN
+    assert f(FAKE, FAKE, FAKE, FAKE, 1, 24, 4608, 64, 4608 * hd, 128, hd, FAKE, ws + 4 * 256, None) == \
+        _lib.FLK_E_UNSUPPORTED
+    assert f(FAKE, FAKE, FAKE, FAKE, 0, 24, 4608, 128, 4608 * hd, 128, hd, None, 0, None) == _lib.FLK_OK  # empty
+    with pytest.raises(_lib.HipKernelError):
+        _lib.check(lib.flk_attend_balanced_plan(1, -1, 10, ctypes.byref(ctypes.c_int()), ctypes.byref(ctypes.c_int64()),
+                                                ctypes.byref(ctypes.c_int64())), "flk_attend_balanced_plan")
+
+
 def test_attend_split_static_validation(lib):
     """flk_attend_split_static_to refuses, before launching anything, split counts out of range
     and calls whose partials would not fit its fixed buffer; every split flk_attend_plan picks
