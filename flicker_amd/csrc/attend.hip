@@ -163,11 +163,11 @@ __device__ __forceinline__ bf16x8 p_operand(const uint32_t (&p)[8], int g) {
 // turns S(u) into P(u) and l.  k_cur / v_cur hold K(u+1) and V(u-1); k_next holds K(u+2),
 // whose first kLead operands (those of the next phase) are read at the end of this one.
 // Element n of a unit is register n % 4 of accumulator n / 4 = g * 2 + kt.
-template <bool kMask>
+template <bool kMask, typename SlotHook>
 __device__ __forceinline__ void phase(WaveState& w, const f32x4 (&s_cur)[4], f32x4 (&s_next)[4],
                                       const uint32_t (&p_prev)[8], uint32_t (&p_cur)[8],
                                       const uint8_t* k_cur, const uint8_t* v_cur, const uint8_t* k_next,
-                                      int key_base, int length, int h) {
+                                      int key_base, int length, int h, SlotHook&& hook) {
   f32x4 sv[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -217,6 +217,7 @@ __device__ __forceinline__ void phase(WaveState& w, const f32x4 (&s_cur)[4], f32
     if (n + 2 < 16) mul(n + 2);
     if (n + 1 < 16) ex(n + 1);
     if (n & 1) pack(n - 1);
+    hook(n);   // the iteration's tile copies, one instruction on some slots
     __builtin_amdgcn_sched_barrier(0);
   }
 }
@@ -230,18 +231,36 @@ struct CopyPlan {
   int lds_wave_off;                   // this wave's rows within a tile (bytes, wave-uniform)
 };
 
+// One tile copy, planned once and issued as kDmaPerTensor instructions (each 4 rows of the
+// wave's 8).  The last tile's offsets are chosen per lane by a select, not a branch.
+struct TileCopy {
+  const uint16_t* base;
+  uint8_t* dst;
+  uint32_t off[kDmaPerTensor];
+};
+
+__device__ __forceinline__ TileCopy plan_copy(uint8_t* dst, const uint16_t* __restrict__ head, int tile,
+                                              const CopyPlan& cp) {
+  tile = min(tile, cp.last_tile);
+  TileCopy tc;
+  tc.base = head + (int64_t)tile * kBN * kD;
+  tc.dst = dst + cp.lds_wave_off;
+  const bool last = tile == cp.last_tile;
+#pragma unroll
+  for (int i = 0; i < kDmaPerTensor; ++i) tc.off[i] = last ? cp.voff_last[i] : cp.voff[i];
+  return tc;
+}
+
+__device__ __forceinline__ void issue_copy(const TileCopy& tc, int i) {
+  flk::dma16_at(tc.base, tc.off[i], tc.dst + i * 4 * kRowBytes);
+}
+
+// Copy 64-key tile `tile` (clamped to the last one) of K or V into an LDS ring slot at once.
 __device__ __forceinline__ void copy_tile(uint8_t* dst, const uint16_t* __restrict__ head, int tile,
                                           const CopyPlan& cp) {
-  tile = min(tile, cp.last_tile);
-  const uint16_t* base = head + (int64_t)tile * kBN * kD;
-  if (tile < cp.last_tile) {
+  const TileCopy tc = plan_copy(dst, head, tile, cp);
 #pragma unroll
-    for (int i = 0; i < kDmaPerTensor; ++i) flk::dma16_at(base, cp.voff[i], dst + cp.lds_wave_off + i * 4 * kRowBytes);
-  } else {
-#pragma unroll
-    for (int i = 0; i < kDmaPerTensor; ++i)
-      flk::dma16_at(base, cp.voff_last[i], dst + cp.lds_wave_off + i * 4 * kRowBytes);
-  }
+  for (int i = 0; i < kDmaPerTensor; ++i) issue_copy(tc, i);
 }
 
 struct Ctx {
@@ -257,18 +276,39 @@ struct Ctx {
 // t+2 into the slots of K tile t-1 and V tile t-2, which no read of this iteration touches.
 // Called with a literal r in the unrolled main loop, so every LDS address folds to a
 // per-lane constant plus an immediate offset.
+// Slots at which the copy instructions of iteration t issue (K's, then V's; 0-15 in phase
+// 2t, 16-31 in phase 2t+1): one at a time between MFMAs rather than all four at the top of
+// the iteration (1.3% faster at 4608 keys than the block of four, measured).
+constexpr int kDmaSlot[kDmaPerIter] = {1, 3, 17, 19};
+
 template <bool kMask>
 __device__ __forceinline__ void iteration(WaveState& w, const Ctx& c, int t, int r) {
-  copy_tile(c.smem + kKRing + ((r + 3) & 3) * kTileBytes, c.kh, t + 3, c.cp);
-  copy_tile(c.smem + kVRing + ((r + 2) & 3) * kTileBytes, c.vh, t + 2, c.cp);
+  const TileCopy kc = plan_copy(c.smem + kKRing + ((r + 3) & 3) * kTileBytes, c.kh, t + 3, c.cp);
+  const TileCopy vc = plan_copy(c.smem + kVRing + ((r + 2) & 3) * kTileBytes, c.vh, t + 2, c.cp);
+  auto hook_a = [&](int n) {
+#pragma unroll
+    for (int i = 0; i < kDmaPerIter; ++i)
+      if (kDmaSlot[i] == n) {
+        if (i < kDmaPerTensor) issue_copy(kc, i);
+        else issue_copy(vc, i - kDmaPerTensor);
+      }
+  };
+  auto hook_b = [&](int n) {
+#pragma unroll
+    for (int i = 0; i < kDmaPerIter; ++i)
+      if (kDmaSlot[i] == n + 16) {
+        if (i < kDmaPerTensor) issue_copy(kc, i);
+        else issue_copy(vc, i - kDmaPerTensor);
+      }
+  };
   const uint8_t* k_t = c.smem + r * kTileBytes;                          // K tile t (less kKRing)
   const uint8_t* k_t1 = c.smem + ((r + 1) & 3) * kTileBytes;             // K tile t+1 (less kKRing)
   const uint8_t* v_t = c.smem + kVRing + r * kTileBytes;                 // V tile t
   const uint8_t* v_tm1 = c.smem + kVRing + ((r + 3) & 3) * kTileBytes;   // V tile t-1
   const int key0 = t * kBN;
   // phase 2t: K(2t+1), V(2t-1), next K(2t+2); phase 2t+1: K(2t+2), V(2t), next K(2t+3)
-  phase<kMask>(w, w.sA, w.sB, w.pB, w.pA, k_t + kUnitBytes, v_tm1 + kUnitBytes, k_t1, key0, c.length, c.h);
-  phase<kMask>(w, w.sB, w.sA, w.pA, w.pB, k_t1, v_t, k_t1 + kUnitBytes, key0 + 32, c.length, c.h);
+  phase<kMask>(w, w.sA, w.sB, w.pB, w.pA, k_t + kUnitBytes, v_tm1 + kUnitBytes, k_t1, key0, c.length, c.h, hook_a);
+  phase<kMask>(w, w.sB, w.sA, w.pA, w.pB, k_t1, v_t, k_t1 + kUnitBytes, key0 + 32, c.length, c.h, hook_b);
   // Wait for the copies started one iteration ago, then a plain s_barrier: the LDS reads
   // still in flight touch no buffer the next copies write, so no lgkmcnt wait is needed.
   asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" :: "n"(kDmaPerIter) : "memory");
