@@ -65,6 +65,8 @@ def parse():
     ap.add_argument("--kernel-launches", type=int, default=200,
                     help="back-to-back launches of each kernel alone behind its average launch duration")
     ap.add_argument("--workload", default="klein_1024")
+    ap.add_argument("--eager-kernel-timing", action="store_true",
+                    help="time each kernel leg as eager back-to-back launches instead of a replayed HIP graph")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-w8a8", action="store_true", help="skip the int8 W8A8 QKV projection leg")
     ap.add_argument("--projection", default="qkv_1024")
@@ -258,7 +260,8 @@ def w8a8_leg(args, timed, dev) -> dict:
     ys = [torch.empty((p.tokens, p.out_features), dtype=torch.bfloat16, device=dev) for _ in range(2)]
     for i in range(20):
         w8a8.gemm(xq, a_scale, qw.wq_t, qw.w_scale, out=ys[i % 2])
-    gemm_ms = timed(lambda i: w8a8.gemm(xq, a_scale, qw.wq_t, qw.w_scale, out=ys[i % 2]), args.kernel_launches)
+    gemm_ms = timed(lambda i: w8a8.gemm(xq, a_scale, qw.wq_t, qw.w_scale, out=ys[i % 2]), args.kernel_launches,
+                    "w8a8_gemm")
     quant_ms = timed(lambda i: w8a8.quantize_act(x, qw.inv_smooth), args.kernel_launches)
     tops = p.gemm_ops() / (gemm_ms * 1e-3) / 1e12
     # The projection feeding qk_prep: the GEMM + qk_prep pair, and the fused kernel whose
@@ -276,10 +279,10 @@ def w8a8_leg(args, timed, dev) -> dict:
                for _ in range(2)]
     x3 = x.view(1, p.tokens, p.hidden)
     lib = __import__("flicker_amd._lib", fromlist=["lib"])
-    stream = lib.stream_of(x)
 
     def fused(i):
         o = qkv_out[i % 2]
+        stream = lib.stream_of(x)   # the current stream at call time (a capture stream under graph timing)
         lib.check(lib.lib().flk_w8a8_qk_prep(
             xq.data_ptr(), qw.wq_t.data_ptr(), a_scale.data_ptr(), qw.w_scale.data_ptr(), p.hidden,
             freqs.cos.data_ptr(), freqs.sin.data_ptr(), freqs.cos.stride(0), qs.data_ptr(), ks.data_ptr(), 0,
@@ -291,7 +294,7 @@ def w8a8_leg(args, timed, dev) -> dict:
         w8a8.gemm(xq, a_scale, qw.wq_t, qw.w_scale, out=y)
         kernels.qk_prep(y.view(1, p.tokens, p.out_features), qs, ks, freqs, heads, out=qkv_out[i % 2])
 
-    fused_ms = timed(fused, args.kernel_launches)
+    fused_ms = timed(fused, args.kernel_launches, "w8a8_qk_prep_fused")
     unfused_ms = timed(unfused, args.kernel_launches)
     # The block input's modulate (LayerNorm, scale, shift) fused into the quantisation.
     g = torch.Generator().manual_seed(6)
@@ -440,7 +443,7 @@ def main() -> int:
         if calib_gemm is not None:
             calib_gemm()
 
-    def timed(fn, n):
+    def timed(fn, n, name=None):
         """Average ms per call of n back-to-back calls between one pair of HIP events on the
         launch stream (torch's current stream, which the kernels are enqueued on)."""
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -450,6 +453,34 @@ def main() -> int:
         e1.record()
         e1.synchronize()
         return e0.elapsed_time(e1) / n
+
+    def timed_graph(fn, n):
+        """Average ms per call of fn with 2 * n_sets calls (every buffer set twice) captured
+        into one HIP graph, replayed until about n calls have run, between one pair of HIP
+        events.  Leaves out the Python enqueue of each call, which is longer than a short
+        kernel (~16 us for qk_prep's host-side checks) and would otherwise be what is timed."""
+        calls = 2 * n_sets
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):   # first calls outside the capture (allocator, plans)
+            for i in range(calls):
+                fn(i)
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for i in range(calls):
+                fn(i)
+        graph.replay()
+        torch.cuda.synchronize()
+        reps = max(1, -(-n // calls))
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            graph.replay()
+        e1.record()
+        e1.synchronize()
+        return e0.elapsed_time(e1) / (reps * calls)
 
     for i in range(args.warmup):
         step(i)
@@ -466,12 +497,26 @@ def main() -> int:
     clock_warmup_s = time.perf_counter() - clock_t0 if clock_steps else 0.0
     step_ms = timed(step, args.steps)
     # Per-kernel launch durations: each kernel alone, back to back over the same rotating
-    # buffers (what a rocprofv3 kernel trace of the same command reports per dispatch).
+    # buffers in a replayed HIP graph (what a rocprofv3 kernel trace of the same command
+    # reports per dispatch, plus the small gaps between graph nodes).
     n_kernel = args.kernel_launches
-    qk_ms = timed(run_qk, n_kernel) if args.only == "step" else step_ms
-    at_ms = timed(run_attend, n_kernel) if args.only == "step" else step_ms
+    legs = {}   # per-leg (eager, graph) ms, for the record
+
+    def timed_min(fn, n, name=None):
+        """The smaller of the two GPU-inclusive timings: eager back-to-back launches (exact
+        when the GPU is the bottleneck, inflated by the Python enqueue for short kernels) and
+        a replayed HIP graph (no enqueue, but ~2 us between graph nodes)."""
+        eager = timed(fn, n)
+        graph = timed_graph(fn, n)
+        if name:
+            legs[name] = {"eager_us": round(eager * 1e3, 2), "graph_us": round(graph * 1e3, 2)}
+        return min(eager, graph)
+
+    kernel_timed = timed if args.eager_kernel_timing else timed_min
+    qk_ms = kernel_timed(run_qk, n_kernel, "qk_prep") if args.only == "step" else step_ms
+    at_ms = kernel_timed(run_attend, n_kernel, "attend") if args.only == "step" else step_ms
     qk_gbs = w.qk_prep_bytes() / (qk_ms * 1e-3) / 1e9
-    qk_ids_ms = timed(run_qk_ids, n_kernel) if args.only == "step" else None
+    qk_ids_ms = kernel_timed(run_qk_ids, n_kernel, "qk_prep_ids") if args.only == "step" else None
     at_tflops = w.attend_flops() / (at_ms * 1e-3) / 1e12
 
     def p50_launch_us(fn, reps: int = 30) -> float:
@@ -518,6 +563,9 @@ def main() -> int:
         "clock_warmup_s": round(clock_warmup_s, 2),
         "clock_warmup_steps": clock_steps,
         "kernel_launches": n_kernel if args.only == "step" else None,
+        "kernel_timing": "eager back-to-back launches" if args.eager_kernel_timing else
+                         "min of eager back-to-back launches and a replayed HIP graph",
+        "kernel_timings": legs or None,
         "ms_per_step": round(step_ms, 4),
         "higher_is_better": True,
         "scaling": "weak",
@@ -548,9 +596,9 @@ def main() -> int:
             "avg_launch_us": round(qk_ids_ms * 1e3, 2), "bytes_per_launch": w.qk_prep_bytes(tables=False),
             "achieved": round(ids_gbs, 1), "unit": "GB/s", "frac": round(ids_gbs / HBM_PEAK_GBS, 4)}
     if args.only == "step" and w.num_heads % SHARE_GPUS == 0:
-        result["head_share"] = head_share_leg(w, sets[0][1], timed)
+        result["head_share"] = head_share_leg(w, sets[0][1], kernel_timed)
     if not args.no_w8a8 and args.only == "step":
-        result["w8a8"] = w8a8_leg(args, timed, dev)
+        result["w8a8"] = w8a8_leg(args, kernel_timed, dev)
         proj = workloads.PROJECTIONS[args.projection]
         result["w8a8"]["roofline"].update(mfma_fields("w8a8_gemm"))
         result["w8a8"]["roofline"]["bytes_per_launch"] = proj.gemm_bytes()

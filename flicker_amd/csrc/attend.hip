@@ -590,11 +590,12 @@ __global__ __launch_bounds__(kThreads, 2) void attend_kernel(
 // each segment's fixed cost.  The last round then costs about f / ntiles of a tile instead
 // of a whole one (half a tile when the helpers outnumber the leftover tiles, m = 1).
 //
-// Each cut tile has exactly two pieces, which write their (acc, l) partials to its two slots
-// with coherent stores and, once those have completed, increment its counter; the piece that
-// finds the counter at 1 is second: it adds the other piece's partial to its own registers
-// (a + b = b + a, so the result does not depend on the order of arrival), writes O and resets
-// the counter to 0 for the next launch.  No block ever waits for another.  A device-scope
+// Each cut tile has exactly two pieces.  The first to finish writes its (acc, l) partial to
+// its slot with coherent stores and, once those have completed, increments the tile's
+// counter; the second finds the counter at 1 (before or by its own increment), adds the
+// other piece's partial to its own registers (a + b = b + a, so the result does not depend
+// on the order of arrival), writes O and resets the counter to 0 for the next launch.  No
+// block ever waits for another.  A device-scope
 // fence here would write back and invalidate the whole L2 of the XCD for every piece, which
 // stalls every block streaming keys through that L2 (tens of microseconds per fence).
 struct BalancedPlan {
@@ -649,23 +650,32 @@ __global__ __launch_bounds__(kThreads, 2) void attend_balanced_kernel(
     if (!cut || l < xs.r) nleft = l < xs.r ? 1 : 0;
     else nleft = hh < xs.r ? (xs.r - 1 - hh) / xs.h + 1 : 0;
   }
-  for (int sg = 0; sg < xs.R + nleft; ++sg) {
-    int unit, t0 = 0, t1 = bp.ntiles, slot = -1, piece = 0;
+  struct Segment {
+    int unit, t0, t1, slot, piece;
+  };
+  auto segment = [&](int sg) {
+    Segment g{0, 0, bp.ntiles, -1, 0};
     if (sg < xs.R) {
-      unit = xs.ux0 + sg * C + l;
+      g.unit = xs.ux0 + sg * C + l;
     } else if (!cut) {
-      unit = left0 + l;
+      g.unit = left0 + l;
     } else if (l < xs.r) {
-      unit = left0 + l;
-      t1 = xs.f;
-      slot = x * C + l;
+      g.unit = left0 + l;
+      g.t1 = xs.f;
+      g.slot = x * C + l;
     } else {
       const int i = hh + (sg - xs.R) * xs.h;
-      unit = left0 + i;
-      t0 = xs.f;
-      slot = x * C + i;
-      piece = 1;
+      g.unit = left0 + i;
+      g.t0 = xs.f;
+      g.slot = x * C + i;
+      g.piece = 1;
     }
+    return g;
+  };
+  const int nseg = xs.R + nleft;
+  for (int sg = 0; sg < nseg; ++sg) {
+    const Segment g = segment(sg);
+    const int unit = g.unit, t0 = g.t0, t1 = g.t1, slot = g.slot, piece = g.piece;
     const int bh = unit / q_blocks, qblk = unit - bh * q_blocks;
     __syncthreads();   // every wave is done with the previous segment's LDS
     WaveState w;
@@ -676,21 +686,27 @@ __global__ __launch_bounds__(kThreads, 2) void attend_balanced_kernel(
       store_o(w, ls, o, bh, heads, qblk, length, o_batch_stride, o_head_stride, o_row_stride);
       continue;
     }
-    // Hand-off without a cache-wide fence: the partial goes out as coherent stores, the
-    // wave waits until they have completed (vmcnt counts them until the memory system has
-    // acknowledged them), the barrier then orders every wave's completed stores before the
-    // counter increment.  The second arriver's coherent loads issue only after its increment
-    // has returned 1, i.e. after both pieces' stores completed.
-    store_partial<true>(w, ls, part_acc, part_l, (int64_t)slot * 2 + piece);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    // Hand-off without a cache-wide fence.  A piece that finds the other already published
+    // (counter 1) merges at once and stores no partial of its own.  Otherwise its partial goes
+    // out as coherent stores, the wave waits until they have completed (vmcnt counts them
+    // until the memory system has acknowledged them), the barrier orders every wave's
+    // completed stores before the counter increment, and the increment says whether the
+    // other piece published in the meantime (1: merge) or not (0: the other piece merges).
+    // Coherent loads of the other partial issue only after a 1 was seen, i.e. after the
+    // other piece's stores completed.
+    if (threadIdx.x == 0) arrival = __hip_atomic_load(&counters[slot], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
-    if (threadIdx.x == 0) arrival = atomicAdd(&counters[slot], 1);
-    __syncthreads();
-    if (arrival == 1) {   // second: add the other piece's partial, write O
-      add_partial(w, ls, part_acc, part_l, (int64_t)slot * 2 + (1 - piece));
-      store_o(w, ls, o, bh, heads, qblk, length, o_batch_stride, o_head_stride, o_row_stride);
-      if (threadIdx.x == 0) counters[slot] = 0;
+    if (arrival == 0) {
+      store_partial<true>(w, ls, part_acc, part_l, (int64_t)slot * 2 + piece);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      if (threadIdx.x == 0) arrival = atomicAdd(&counters[slot], 1);
+      __syncthreads();
+      if (arrival == 0) continue;   // first to publish: the other piece writes O
     }
+    add_partial(w, ls, part_acc, part_l, (int64_t)slot * 2 + (1 - piece));
+    store_o(w, ls, o, bh, heads, qblk, length, o_batch_stride, o_head_stride, o_row_stride);
+    if (threadIdx.x == 0) counters[slot] = 0;
   }
 }
 
