@@ -512,28 +512,6 @@ __device__ __forceinline__ void store_partial(const WaveState& w, const float (&
   }
 }
 
-// Adds the partial that store_partial<true> wrote to `slot` into the wave's registers, with
-// relaxed device-scope atomic loads (coherent with those stores).
-__device__ __forceinline__ void add_partial(WaveState& w, float (&l)[2], const float* __restrict__ part_acc,
-                                            const float* __restrict__ part_l, int64_t slot) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int64_t ws = slot * kWaves + wave;
-  const f32x4* src = reinterpret_cast<const f32x4*>(part_acc) + ws * 1024 + lane;
-#pragma unroll
-  for (int dt = 0; dt < 8; ++dt)
-#pragma unroll
-    for (int g = 0; g < 2; ++g) {
-      const uint64_t* s = reinterpret_cast<const uint64_t*>(src + (dt * 2 + g) * 64);
-      union { f32x4 f; uint64_t u[2]; } x;
-      x.u[0] = __hip_atomic_load(s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      x.u[1] = __hip_atomic_load(s + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      w.oacc[dt][g] += x.f;
-    }
-#pragma unroll
-  for (int g = 0; g < 2; ++g)
-    l[g] += __hip_atomic_load(part_l + ws * 64 + g * 16 + (lane & 15), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 // kSplit = false: the block takes every key of its 256 queries and writes O.
 // kSplit = true: the key tiles are cut into `splits` ranges of equal length (+-1 tile); the
 // block takes one range and writes its unnormalised acc and l to part_acc / part_l, which
@@ -583,49 +561,68 @@ __global__ __launch_bounds__(kThreads, 2) void attend_kernel(
 // contiguous ranges (keeping each head's K/V in one L2).  On an XCD with n tiles and C = 32
 // CUs, CU l first takes tiles l, l + C, ... whole for R = floor(n / C) rounds -- the plain
 // kernel's rounds, every CU streaming the keys from tile 0 together, so that K/V tiles are
-// shared in the L2 as they arrive.  The r = n - R C tiles left over are cut by keys: CU l < r
-// takes the first f key tiles of leftover tile l, and the other h = C - r CUs ("helpers") take
-// the rest [f, ntiles) of the leftover tiles, helper j those with index = j mod h -- at most
-// m = ceil(r / h) each, with f chosen so that no helper outlasts the first parts, counting
-// each segment's fixed cost.  The last round then costs about f / ntiles of a tile instead
-// of a whole one (half a tile when the helpers outnumber the leftover tiles, m = 1).
+// shared in the L2 as they arrive.  The r = n - R C tiles left over are W = r * ntiles key
+// tiles of work, laid end to end and cut into P = min(C, W) equal ranges, one per CU l < P
+// (floor(W l / P) to floor(W (l + 1) / P)): every range is shorter than a tile, so it spans
+// at most two segments, and a leftover tile is covered by the ranges of CUs cf .. cl.
 //
-// Each cut tile has exactly two pieces.  The first to finish writes its (acc, l) partial to
-// its slot with coherent stores and, once those have completed, increments the tile's
-// counter; the second finds the counter at 1 (before or by its own increment), adds the
-// other piece's partial to its own registers (a + b = b + a, so the result does not depend
-// on the order of arrival), writes O and resets the counter to 0 for the next launch.  No
-// block ever waits for another.  A device-scope
-// fence here would write back and invalidate the whole L2 of the XCD for every piece, which
-// stalls every block streaming keys through that L2 (tens of microseconds per fence).
-struct BalancedPlan {
-  int units, ntiles, grid;
-};
-
-// The leftover split of an XCD with n tiles: rounds R, leftover r, helpers h, first-part
-// length f (f == ntiles: the leftover tiles are not cut, each runs whole on CU l < r).
-// Fixed cost of one segment in key tiles: its prologue (Q and the first K/V tiles from
-// memory, ~4.5 us when every CU starts at once) plus the partial hand-off (~4 us), against
-// ~1.5 us per key tile (measured at 4608 keys).
-constexpr int kSegmentTiles = 6;
-
+// A tile covered by one range is written directly.  Otherwise each of its pieces, when its
+// segment ends, either finds the tile's counter at pieces - 1 (every other piece published)
+// or publishes its (acc, l) partial: coherent stores to its slot, a wait until they have
+// completed, then the counter increment -- whose old value says whether it was the last.
+// The last piece sums all the pieces in CU order, ((p0 + p1) + p2) + ..., so the result does
+// not depend on the order of arrival (its own piece from registers when it is p0 or p1,
+// whose sum is the same either way; otherwise it publishes too and reads its own back), writes
+// O and resets the counter to 0 for the next launch.  No block ever waits for another.  A device-scope fence here would write back and
+// invalidate the whole L2 of the XCD for every piece, which stalls every block streaming
+// keys through that L2 (tens of microseconds per fence).
 struct XcdSplit {
-  int ux0, R, r, h, f;
+  int ux0, R, r, P;
+  int W;   // leftover key tiles (< 32 ntiles; the host keeps 1024 ntiles below 2^31)
 };
 
-__device__ __forceinline__ XcdSplit xcd_split(const BalancedPlan& bp, int x) {
+__device__ __forceinline__ XcdSplit xcd_split(int units, int ntiles, int x) {
   constexpr int C = kCUs / kXcds;
   XcdSplit xs;
-  xs.ux0 = (int)((int64_t)x * bp.units / kXcds);
-  const int n = (int)((int64_t)(x + 1) * bp.units / kXcds) - xs.ux0;
+  xs.ux0 = (int)((int64_t)x * units / kXcds);
+  const int n = (int)((int64_t)(x + 1) * units / kXcds) - xs.ux0;
   xs.R = n / C;
   xs.r = n - xs.R * C;
-  xs.h = C - xs.r;
-  const int m = xs.r > 0 ? (xs.r + xs.h - 1) / xs.h : 1;
-  // First part f + s against m second parts m (ntiles - f + s), s = a segment's fixed cost in
-  // key tiles: f = ceil((m ntiles + (m - 1) s) / (m + 1)), at most ntiles (then no cut).
-  xs.f = min(bp.ntiles, (m * bp.ntiles + (m - 1) * kSegmentTiles + m) / (m + 1));
+  xs.W = xs.r * ntiles;
+  xs.P = min(C, xs.W);
   return xs;
+}
+
+// Start of leftover range c (key tiles), c = 0 .. P.
+__device__ __forceinline__ int range_start(const XcdSplit& xs, int c) { return xs.W * c / xs.P; }
+
+// The range that holds leftover key tile u: the largest c with range_start(c) <= u.
+__device__ __forceinline__ int range_of(const XcdSplit& xs, int u) { return (xs.P * (u + 1) - 1) / xs.W; }
+
+// Adds (or, first, assigns) the partial in `slot` to res / rl: res + p in f32, the order of
+// the fold.  Read with relaxed device-scope atomic loads (coherent with store_partial<true>).
+__device__ __forceinline__ void gather_partial(f32x4 (&res)[8][2], float (&rl)[2], bool first,
+                                               const float* __restrict__ part_acc,
+                                               const float* __restrict__ part_l, int64_t slot) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t ws = slot * kWaves + wave;
+  const f32x4* src = reinterpret_cast<const f32x4*>(part_acc) + ws * 1024 + lane;
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      const uint64_t* s = reinterpret_cast<const uint64_t*>(src + (dt * 2 + g) * 64);
+      union { f32x4 f; uint64_t u[2]; } x;
+      x.u[0] = __hip_atomic_load(s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      x.u[1] = __hip_atomic_load(s + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      res[dt][g] = first ? x.f : res[dt][g] + x.f;
+    }
+#pragma unroll
+  for (int g = 0; g < 2; ++g) {
+    const float v = __hip_atomic_load(part_l + ws * 64 + g * 16 + (lane & 15), __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT);
+    rl[g] = first ? v : rl[g] + v;
+  }
 }
 
 __global__ __launch_bounds__(kThreads, 2) void attend_balanced_kernel(
@@ -637,76 +634,64 @@ __global__ __launch_bounds__(kThreads, 2) void attend_balanced_kernel(
   __shared__ int arrival;
   constexpr int C = kCUs / kXcds;
   const int x = blockIdx.x % kXcds, l = blockIdx.x / kXcds;   // hardware deals blocks round-robin over XCDs
-  const BalancedPlan bp{units, (length + kBN - 1) / kBN, (int)gridDim.x};
-  const XcdSplit xs = xcd_split(bp, x);
-
-  // This block's segments: R whole tiles, then its leftover pieces (one first part, or up to
-  // m second parts, or -- when the tiles are too short to cut -- one whole leftover tile).
+  const int ntiles = (length + kBN - 1) / kBN;
+  const XcdSplit xs = xcd_split(units, ntiles, x);
   const int left0 = xs.ux0 + xs.R * C;   // first leftover tile of this XCD
-  const bool cut = xs.f < bp.ntiles;
-  const int hh = l - xs.r;               // helper index (>= 0 for helpers)
-  int nleft = 0;
-  if (xs.r > 0) {
-    if (!cut || l < xs.r) nleft = l < xs.r ? 1 : 0;
-    else nleft = hh < xs.r ? (xs.r - 1 - hh) / xs.h + 1 : 0;
-  }
-  struct Segment {
-    int unit, t0, t1, slot, piece;
-  };
-  auto segment = [&](int sg) {
-    Segment g{0, 0, bp.ntiles, -1, 0};
+
+  // Segments: the whole tiles of the full rounds, then this CU's leftover range, one
+  // segment per tile it touches (i = the leftover tile, -1 for a whole tile).
+  int u = l < xs.P ? range_start(xs, l) : 0;
+  const int u_end = l < xs.P ? range_start(xs, l + 1) : 0;
+  for (int sg = 0;; ++sg) {
+    int unit, t0 = 0, t1 = ntiles, i = -1;
     if (sg < xs.R) {
-      g.unit = xs.ux0 + sg * C + l;
-    } else if (!cut) {
-      g.unit = left0 + l;
-    } else if (l < xs.r) {
-      g.unit = left0 + l;
-      g.t1 = xs.f;
-      g.slot = x * C + l;
+      unit = xs.ux0 + sg * C + l;
     } else {
-      const int i = hh + (sg - xs.R) * xs.h;
-      g.unit = left0 + i;
-      g.t0 = xs.f;
-      g.slot = x * C + i;
-      g.piece = 1;
+      if (u >= u_end) break;
+      i = u / ntiles;
+      t0 = u - i * ntiles;
+      t1 = min(ntiles, t0 + (u_end - u));
+      u += t1 - t0;
+      unit = left0 + i;
     }
-    return g;
-  };
-  const int nseg = xs.R + nleft;
-  for (int sg = 0; sg < nseg; ++sg) {
-    const Segment g = segment(sg);
-    const int unit = g.unit, t0 = g.t0, t1 = g.t1, slot = g.slot, piece = g.piece;
     const int bh = unit / q_blocks, qblk = unit - bh * q_blocks;
     __syncthreads();   // every wave is done with the previous segment's LDS
     WaveState w;
     attend_segment(w, smem, q, k, v, length, bh, qblk, t0, t1);
     float ls[2];
     row_sums(w, ls);
-    if (slot < 0) {
+    const int cf = i < 0 ? 0 : range_of(xs, i * ntiles);
+    const int cl = i < 0 ? 0 : range_of(xs, (i + 1) * ntiles - 1);
+    if (cf == cl) {   // a whole tile of one range
       store_o(w, ls, o, bh, heads, qblk, length, o_batch_stride, o_head_stride, o_row_stride);
       continue;
     }
-    // Hand-off without a cache-wide fence.  A piece that finds the other already published
-    // (counter 1) merges at once and stores no partial of its own.  Otherwise its partial goes
-    // out as coherent stores, the wave waits until they have completed (vmcnt counts them
-    // until the memory system has acknowledged them), the barrier orders every wave's
-    // completed stores before the counter increment, and the increment says whether the
-    // other piece published in the meantime (1: merge) or not (0: the other piece merges).
-    // Coherent loads of the other partial issue only after a 1 was seen, i.e. after the
-    // other piece's stores completed.
-    if (threadIdx.x == 0) arrival = __hip_atomic_load(&counters[slot], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int others = cl - cf, pos = l - cf;
+    auto slot_of = [&](int c) {
+      return (int64_t)(x * C + c) * 2 + (i - range_start(xs, c) / ntiles);
+    };
+    int* counter = &counters[x * C + i];
+    if (threadIdx.x == 0) arrival = __hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
-    if (arrival == 0) {
-      store_partial<true>(w, ls, part_acc, part_l, (int64_t)slot * 2 + piece);
+    // Publish unless every other piece already has and this piece is one of the first two
+    // (whose sum is the same in either order, so it can start from its registers).
+    if (arrival < others || pos >= 2) {
+      store_partial<true>(w, ls, part_acc, part_l, slot_of(l));
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();   // every wave's stores have completed before the increment
+      if (threadIdx.x == 0) arrival = atomicAdd(counter, 1);
       __syncthreads();
-      if (threadIdx.x == 0) arrival = atomicAdd(&counters[slot], 1);
-      __syncthreads();
-      if (arrival == 0) continue;   // first to publish: the other piece writes O
+      if (arrival < others) continue;   // a later piece writes O
     }
-    add_partial(w, ls, part_acc, part_l, (int64_t)slot * 2 + (1 - piece));
+    // Last piece: O = ((p_cf + p_cf+1) + p_cf+2) + ..., the pieces in CU order.
+    if (pos <= 1) {
+      gather_partial(w.oacc, ls, false, part_acc, part_l, slot_of(pos == 0 ? cf + 1 : cf));
+      for (int c = cf + 2; c <= cl; ++c) gather_partial(w.oacc, ls, false, part_acc, part_l, slot_of(c));
+    } else {
+      for (int c = cf; c <= cl; ++c) gather_partial(w.oacc, ls, c == cf, part_acc, part_l, slot_of(c));
+    }
     store_o(w, ls, o, bh, heads, qblk, length, o_batch_stride, o_head_stride, o_row_stride);
-    if (threadIdx.x == 0) counters[slot] = 0;
+    if (threadIdx.x == 0) *counter = 0;
   }
 }
 
@@ -836,7 +821,7 @@ int64_t balanced_workspace_bytes(int grid) { return balanced_counters_offset(gri
 bool balanced_preferred(int batch, int heads, int length) {
   const int64_t units = q_tiles(length) * batch * heads;
   constexpr int C = kCUs / kXcds;
-  if (units < kCUs || units > INT32_MAX) return false;
+  if (units < kCUs || units > INT32_MAX || (int64_t)(length + kBN - 1) / kBN * 1024 > INT32_MAX) return false;
   const int64_t left = ((units + kXcds - 1) / kXcds) % C;   // leftover tiles of the fullest XCD
   return left > 0 && left * 8 <= C * 5;
 }
@@ -860,6 +845,7 @@ extern "C" int flk_attend_balanced_to(const void* q, const void* k, const void* 
                               o_row_stride);
   if (st != FLK_OK) return st == kNothing ? FLK_OK : st;
   const int64_t units = q_tiles(length) * batch * heads;   // <= INT32_MAX (check_attend)
+  if ((int64_t)(length + kBN - 1) / kBN * 1024 > INT32_MAX) return FLK_E_UNSUPPORTED;   // 32-bit split math
   constexpr int grid = kCUs;
   if (!workspace || workspace_bytes < balanced_workspace_bytes(grid)) return FLK_E_INVALID;
   if (!flk_host_aligned(workspace, 16)) return FLK_E_ALIGN;

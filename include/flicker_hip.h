@@ -148,12 +148,12 @@ int flk_attend_split_static_to(const void* q, const void* k, const void* v, void
  * (src/flicker/kernels.py:105-145): instead of one block per (b, h, 256-query tile) -- 432
  * tiles at the Klein 1024^2 shape, 1.69 rounds of 256 CUs -- 256 persistent blocks, 32 per
  * XCD.  Each XCD takes a contiguous range of tiles; its CUs do whole tiles for as many full
- * rounds as the range holds, and the tiles left over are cut by keys into two pieces: a
- * first part of f key tiles on one CU and the rest on one of the CUs that had no leftover
- * tile, f chosen so that no CU does more than f.  The two pieces' (acc, l) partials are
- * added by whichever finishes second (plain sums: the reference keeps no running max); no
- * block waits for another.  Only the f32 summation order of the cut tiles differs from
- * flk_attend_to; the results are deterministic for a given shape.
+ * rounds as the range holds, and the key tiles of the tiles left over are laid end to end
+ * and cut into 32 equal ranges, one per CU, so a leftover tile may be shared by a few CUs.
+ * The pieces' (acc, l) partials are summed by whichever piece finishes last, always in the
+ * same order (plain sums: the reference keeps no running max); no block waits for another.
+ * Only the f32 summation order of the shared tiles differs from flk_attend_to; the results
+ * are deterministic for a given shape.
  *   - Takes every shape flk_attend_to takes; flk_attend_balanced_plan says whether it is the
  *     faster launch for a shape.
  *   - `workspace`: caller-owned, 16-byte aligned, at least flk_attend_balanced_plan's bytes.

@@ -1,6 +1,7 @@
-"""The balanced attend (flk_attend_balanced_to: one persistent block per CU; each XCD's tiles
-left over after its full rounds cut by keys into two pieces, merged by whichever piece
-finishes second) against the bounded oracle and against the one-block-per-tile kernel.
+"""The balanced attend (flk_attend_balanced_to: one persistent block per CU; the key tiles of
+each XCD's tiles left over after its full rounds shared out in equal ranges over its CUs, the
+pieces of a tile summed in a fixed order by whichever finishes last) against the bounded
+oracle and against the one-block-per-tile kernel.
 
 Gates: the tight bounded-oracle gate of test_gpu_attend; against flk_attend_to only the cut
 tiles may differ, by the f32 order of two partial sums (at most one bf16 ulp of the largest
@@ -41,9 +42,9 @@ def counters_zero(q):
                                                  (1, 9, 4352), (1, 40, 1000)])
 def test_balanced_matches_oracle(device, batch, heads, length):
     """Exactly 256 (b, h, 256-query tile) units: no cut (L = 1000: a masked last key tile);
-    30 units (fewer than the XCDs' CUs: every tile of an XCD cut); 153 units at 68 key tiles
-    (first part + one or two second parts per helper); 160 units at L = 1000 (cut tiles
-    with a masked last key tile in the second piece)."""
+    30 units (3-4 tiles per XCD: every tile in 8-11 pieces); 153 units at 68 key tiles (19-20
+    tiles per XCD, two pieces each); 160 units at L = 1000 (20 tiles per XCD, pieces ending
+    on the masked last key tile)."""
     print(f"balanced B={batch} H={heads} L={length}", flush=True)
     q, k, v = prepped_case(batch, heads, length, seed=length + heads)
     qd, kd, vd = (t.to(device) for t in (q, k, v))
