@@ -119,3 +119,32 @@ def test_balanced_graph_replay(device):
         torch.cuda.synchronize()
         assert torch.equal(static_o, want)
         assert eager.shape == want.shape
+
+
+def test_balanced_ragged_batch_uneven_xcds(device):
+    """B = 2, L = 1100: a partial last query tile (76 rows) and a masked last key tile (12
+    keys); 50 tiles, so the XCDs hold 6 or 7 (units % 8 = 2) and every tile is shared."""
+    q, k, v = prepped_case(2, 5, 1100, seed=21)
+    qd, kd, vd = (t.to(device) for t in (q, k, v))
+    got = run(qd, kd, vd)
+    assert not torch.isnan(got).any()
+    tight_gate("balanced B2 H5 L1100", to_np(got), P.attend_bounded(to_np(q), to_np(k), to_np(v)).astype(np.float64))
+    plain = run(qd, kd, vd, splits=1, balanced=False)
+    scale = float(plain.float().abs().max())
+    assert float((got.float() - plain.float()).abs().max()) <= 2.0 ** (math.floor(math.log2(scale)) - 7)
+    assert counters_zero(qd)
+
+
+def test_balanced_token_major_output(device):
+    """O through the token-major strides of attend_merged (B, L, H*D): the same bits as the
+    head-major output of the same launch, and the rows between heads untouched."""
+    batch, heads, length = 1, 40, 1024
+    q, k, v = (t.to(device) for t in prepped_case(batch, heads, length, seed=22))
+    head_major = run(q, k, v)
+    merged = torch.full((batch, length, heads * D + 8), float("nan"), dtype=torch.bfloat16, device=device)
+    view = merged[..., :heads * D]
+    kernels._launch_attend(q, k, v, view, (merged.stride(0), D, merged.stride(1)), None, True)
+    torch.cuda.synchronize()
+    assert torch.equal(view.view(batch, length, heads, D).transpose(1, 2), head_major)
+    assert torch.isnan(merged[..., heads * D:]).all(), "a store landed past the head columns"
+    assert counters_zero(q)
