@@ -803,9 +803,9 @@ extern "C" int flk_attend_to(const void* q, const void* k, const void* v, void* 
 
 namespace {
 
-// Workspace of a balanced launch on `grid` blocks: two partial slots per cut tile, at most
-// one cut tile per block (acc: 8 waves x 1024 float4; l: 8 waves x 64 floats), then one int
-// counter per cut tile.
+// Workspace of a balanced launch on `grid` blocks: two partial slots per block, one per
+// leftover segment (acc: 8 waves x 1024 float4; l: 8 waves x 64 floats), then one int counter
+// per leftover tile (fewer than 32 per XCD, so `grid` counters).
 constexpr int64_t kSlotAccBytes = (int64_t)kWaves * 1024 * 16;
 constexpr int64_t kSlotLBytes = (int64_t)kWaves * 64 * 4;
 
@@ -815,9 +815,10 @@ int64_t balanced_workspace_bytes(int grid) { return balanced_counters_offset(gri
 // Whether the balanced launch beats one block per tile, by the tiles an XCD has left after
 // its full rounds of 32: it does when every XCD has at least one full round and the last
 // round would leave more than 3/8 of the CUs idle (measured: 11% at 64 or 88 of 256 CUs
-// busy, 7% at 48, 2.5% at 152), and not at 176 of 256 (a plain last round on fewer CUs runs
-// at a higher clock under the power limit, which makes up for the idle CUs, and cutting a
-// tile costs ~9 us per piece) nor with no full round (144 tiles: 47 us against 39 us).
+// busy, 7-9% at 48, 2.5% at 152), and not at 176 of 256 (a plain last round on fewer CUs
+// runs at a higher clock under the power limit, which makes up for the idle CUs, and each
+// shared tile's hand-off costs several microseconds) nor with no full round (144 tiles:
+// 45-49 us against 39 us).
 bool balanced_preferred(int batch, int heads, int length) {
   const int64_t units = q_tiles(length) * batch * heads;
   constexpr int C = kCUs / kXcds;
