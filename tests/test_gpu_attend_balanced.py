@@ -148,3 +148,28 @@ def test_balanced_token_major_output(device):
     assert torch.equal(view.view(batch, length, heads, D).transpose(1, 2), head_major)
     assert torch.isnan(merged[..., heads * D:]).all(), "a store landed past the head columns"
     assert counters_zero(q)
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_three_launches_agree_on_random_shapes(device, seed):
+    """Seeded random shapes (B <= 2, H <= 6, L in [1, 1300]): one block per tile, the key
+    split at its planned (or a forced) range count, and the balanced launch each pass the tight
+    oracle gate, and the split and balanced outputs stay within one bf16 ulp of the plain one."""
+    rng = np.random.default_rng(100 + seed)
+    batch, heads, length = int(rng.integers(1, 3)), int(rng.integers(1, 7)), int(rng.integers(1, 1301))
+    q, k, v = prepped_case(batch, heads, length, seed=1000 + seed)
+    want = P.attend_bounded(to_np(q), to_np(k), to_np(v)).astype(np.float64)
+    qd, kd, vd = (t.to(device) for t in (q, k, v))
+    groups = max(1, -(-length // 256))
+    outs = {"plain": run(qd, kd, vd, splits=1, balanced=False),
+            "split": run(qd, kd, vd, splits=min(groups, int(rng.integers(2, 5))) if groups > 1 else 1,
+                         balanced=False),
+            "balanced": run(qd, kd, vd)}
+    print(f"seed {seed}: B={batch} H={heads} L={length}", flush=True)
+    scale = float(outs["plain"].float().abs().max())
+    for name, got in outs.items():
+        assert not torch.isnan(got).any(), name
+        tight_gate(f"{name} B{batch} H{heads} L{length}", to_np(got), want)
+        d = float((got.float() - outs["plain"].float()).abs().max())
+        assert d <= 2.0 ** (math.floor(math.log2(scale)) - 7), (name, d)
+    assert counters_zero(qd)
