@@ -627,7 +627,8 @@ __global__ __launch_bounds__(kGThreads, 2) void w8a8_gemm_kernel(const GemmGroup
   // wave's 128 x 64 sub-tile.  Rescaled bf16 values go to this wave's 16 KiB of the (now
   // idle) LDS as [m][n] rows of 256 B whose 16-byte chunks are XOR-swizzled by m & 15; then
   // the wave reads back 4 rows per instruction (16 lanes x 16 B per row) and writes each
-  // row's 256 contiguous bytes with 16-byte stores.
+  // row's 256 contiguous bytes with 16-byte nontemporal stores (Y is streamed out: 1-2%
+  // faster, and a qk_prep pass reading Y next measured no slower).
   float am[kGMF];
 #pragma unroll
   for (int mf = 0; mf < kGMF; ++mf) am[mf] = a_scale[min(m0 + wm * kGWaveM + mf * 16 + l16, M - 1)];
@@ -713,7 +714,7 @@ __global__ __launch_bounds__(kGThreads, 2) void w8a8_gemm_kernel(const GemmGroup
     if (m < M && n_lane < N) {
       uint16_t* dst = y + (int64_t)m * y_stride + n_lane;
       if (wide && n_lane + 8 <= N) {
-        *reinterpret_cast<uint4*>(dst) = v;
+        __builtin_nontemporal_store(u32x4{v.x, v.y, v.z, v.w}, reinterpret_cast<u32x4*>(dst));
       } else {
         *reinterpret_cast<uint2*>(dst) = uint2{v.x, v.y};
         if (n_lane + 8 <= N) *reinterpret_cast<uint2*>(dst + 4) = uint2{v.z, v.w};
