@@ -129,6 +129,12 @@ __global__ __launch_bounds__(kThreads) void qk_prep_kernel(
 // before the current round's math, so each lane keeps two rounds in flight while the trig of
 // one token serves kRounds * kHeads heads.  The block's first 64 threads compute the
 // (token-independent) pair frequencies into LDS after the first loads are issued.
+//
+// The trig must not wait for the QKV data.  Loads complete in issue order as far as the
+// wait counter is concerned, so the positions are loaded first, and every load is issued
+// unconditionally (a lane past the end reads the last token's row and stores nothing): a
+// load under a branch makes the compiler wait for all outstanding loads where the paths
+// join, which put the whole frequency -> barrier -> trig chain behind the first round's data.
 template <bool kScaleF32, bool kGain, int kHeads, int kRounds>
 __global__ __launch_bounds__(kThreads) void qk_prep_ids_kernel(
     const uint16_t* __restrict__ qkv, int64_t batch_stride, int64_t row_stride, RopeSource rope,
@@ -143,7 +149,8 @@ __global__ __launch_bounds__(kThreads) void qk_prep_ids_kernel(
   const int h0 = blockIdx.y * kHeads * kRounds;
   const int b = blockIdx.z;
   const bool live = t < length;
-  const uint16_t* row = qkv + (int64_t)b * batch_stride + (int64_t)t * row_stride + lane * 8;
+  const int tl = live ? t : length - 1;
+  const uint16_t* row = qkv + (int64_t)b * batch_stride + (int64_t)tl * row_stride + lane * 8;
 
   uint4 buf[2][3 * kHeads];
   auto load_round = [&](int r, uint4 (&dst)[3 * kHeads]) {
@@ -155,13 +162,13 @@ __global__ __launch_bounds__(kThreads) void qk_prep_ids_kernel(
       dst[3 * i + 2] = load16(row + (int64_t)(2 * num_heads + h) * kHeadDim);
     }
   };
-  if (live) load_round(0, buf[0]);
-  // The token's positions on every axis, loaded now so that no memory latency follows the
-  // block barrier: each lane then picks the axis of each of its pairs.
-  const float* pos = rope.ids + (int64_t)t * rope.ids_stride;
+  // The token's positions on every axis (each lane then picks the axis of each of its pairs),
+  // loaded before the QKV rows; axes past the count re-read axis 0 and go unused.
+  const float* pos = rope.ids + (int64_t)tl * rope.ids_stride;
   float pa[flk::kMaxAxes];
 #pragma unroll
-  for (int a = 0; a < flk::kMaxAxes; ++a) pa[a] = live && a < rope.ax.count ? pos[a] : 0.0f;
+  for (int a = 0; a < flk::kMaxAxes; ++a) pa[a] = pos[a < rope.ax.count ? a : 0];
+  load_round(0, buf[0]);
   if (threadIdx.x < kPairs) {
     int axis;
     pair_freq[threadIdx.x] = flk::pair_omega(threadIdx.x, rope.ax, rope.theta, axis);
@@ -216,7 +223,7 @@ struct Launch {
 };
 
 #ifndef FLK_QK_IDS_ROUNDS
-#define FLK_QK_IDS_ROUNDS 3
+#define FLK_QK_IDS_ROUNDS 2
 #endif
 
 template <bool kScaleF32, bool kGain, bool kIds>
@@ -289,7 +296,8 @@ int dispatch(int hpg, int batch, int scale_is_f32, hipStream_t stream, const Lau
 
 // Heads per 16-lane group.  With tables, two measured best at the Klein shapes (6 loads in
 // flight per lane and 2x more blocks than four heads per group).  With ids, each group
-// computes 4 cos/sin pairs per token, which more heads share.
+// computes 4 cos/sin pairs per token, which more heads share: two rounds of two measured
+// best (three rounds: the same at 1024^2, 1.3 us slower at 512^2, 2 us at 2048^2).
 int heads_per_group(int num_heads, bool ids, int forced) {
   int hpg = (num_heads % 2 == 0) ? 2 : (num_heads % 3 == 0) ? 3 : 1;
   if (ids && num_heads % (2 * FLK_QK_IDS_ROUNDS) == 0) hpg = 2 * FLK_QK_IDS_ROUNDS;

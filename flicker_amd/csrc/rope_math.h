@@ -21,15 +21,21 @@ struct Axes {
   int first_pair[kMaxAxes + 1];  // prefix sums of dim/2
 };
 
-// Axis of a pair index and that pair's frequency omega.
+// Axis of a pair index and that pair's frequency omega.  The axis's fields are picked by
+// selects over constant indices: indexing the (kernel-argument) arrays with a per-lane axis
+// would compile to memory loads, whose wait then also waits for every load issued before.
 __device__ __forceinline__ float pair_omega(int pair, const Axes& ax, float theta, int& axis) {
-  int a = 0;
+  int a = 0, first = ax.first_pair[0], dim = ax.dim[0];
 #pragma unroll
-  for (int i = 1; i < kMaxAxes; ++i)
-    if (i < ax.count && pair >= ax.first_pair[i]) a = i;
+  for (int i = 1; i < kMaxAxes; ++i) {
+    const bool in = i < ax.count && pair >= ax.first_pair[i];
+    a = in ? i : a;
+    first = in ? ax.first_pair[i] : first;
+    dim = in ? ax.dim[i] : dim;
+  }
   axis = a;
-  const int kk = pair - ax.first_pair[a];
-  const float scale = (float)(2 * kk) / (float)ax.dim[a];
+  const int kk = pair - first;
+  const float scale = (float)(2 * kk) / (float)dim;
   return 1.0f / powf(theta, scale);
 }
 
