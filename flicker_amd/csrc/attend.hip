@@ -57,7 +57,10 @@
 //
 // Blocks of 8 waves (two per SIMD) take 256 queries of one (b, h).  Blocks are renumbered
 // so that all query tiles of one head run on the same XCD (hardware deals blocks
-// round-robin over the 8 XCDs), keeping the head's K/V in one L2.
+// round-robin over the 8 XCDs), keeping the head's K/V in one L2.  A grid that fits the
+// 256 CUs in one round either way takes 192-query tiles instead (attend_tile192_kernel):
+// waves 4-7 then hold one query group of 16, so each SIMD holds 48 queries instead of 64
+// and the one round is 3/4 as long (measured 16-20% faster, e.g. 512^2: 144 -> 192 blocks).
 //
 // Small grids (few heads, short sequences) leave CUs idle for the whole launch.  For them
 // the keys are cut into ranges (flk_attend_split_to): each block sums one range into
@@ -113,13 +116,15 @@ typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
 __device__ __forceinline__ int swz(int row) { return ((row & 7) << 1) | ((row >> 3) & 1); }
 
+// A wave's registers for G query groups of 16 (G = 2: 32 queries; G = 1: 16).
+template <int G>
 struct WaveState {
-  bf16x8 qreg[4][2];   // Q^T operand: d step s (32 d), query group g (16 queries)
-  f32x4 oacc[8][2];    // O^T: d tile dt (16 d), query group g
-  f32x4 sA[4], sB[4];  // S^T of consecutive units, accumulator g * 2 + kt (16-key tile kt)
-  uint32_t pA[8], pB[8];  // bf16x2-packed P of consecutive units: word g * 4 + kt * 2 + pair
+  bf16x8 qreg[4][G];   // Q^T operand: d step s (32 d), query group g (16 queries)
+  f32x4 oacc[8][G];    // O^T: d tile dt (16 d), query group g
+  f32x4 sA[2 * G], sB[2 * G];  // S^T of consecutive units, accumulator g * 2 + kt (16-key tile kt)
+  uint32_t pA[4 * G], pB[4 * G];  // bf16x2-packed P of consecutive units: word g * 4 + kt * 2 + pair
   bf16x8 ops[kOpRing]; // operand ring: the A operand of slot n sits in ops[n % kOpRing]
-  f32x4 lacc[2];       // row sums l of query groups 0 and 1 (register 0 of lanes 0-15)
+  f32x4 lacc[G];       // row sums l of the query groups (register 0 of lanes 0-15)
   bf16x8 ones;         // A operand of the row-sum MFMA: row 0 all ones, rows 1-15 zero
   int k_off[4];        // K operand byte offsets within a unit, d steps 0-3 (key tile 1 is 16 rows
                        // further, with the same swizzle)
@@ -135,11 +140,12 @@ __device__ __forceinline__ bf16x8 v_operand(const uint8_t* vunit, int off) {
   return __builtin_bit_cast(bf16x8, both);
 }
 
-// Slot n of a phase issues two MFMAs, one per query group, sharing its A operand: n < 8 is
+// Slot n of a phase issues one MFMA per query group, sharing its A operand: n < 8 is
 // d step n / 2 of S = K Q^T for 16-key tile n % 2 (A = K rows of that tile and d step), n >= 8
 // is d tile n - 8 of O^T += V^T P^T (A = V^T operand of the tile).  The operand is read from
 // LDS kLead slots earlier.
-__device__ __forceinline__ bf16x8 load_operand(const WaveState& w, int n, const uint8_t* k_unit,
+template <int G>
+__device__ __forceinline__ bf16x8 load_operand(const WaveState<G>& w, int n, const uint8_t* k_unit,
                                                const uint8_t* v_unit) {
   if (n < 8) {
     const int st = n >> 1, kt = n & 1;
@@ -155,26 +161,31 @@ __device__ __forceinline__ f32x4 mfma16(const bf16x8& a, const bf16x8& b, const 
 
 // P^T of query group g as the B operand of O^T += V^T P^T: k-slots 0-3 from 16-key tile 0,
 // 4-7 from tile 1 -- the group's four packed words, in order.
-__device__ __forceinline__ bf16x8 p_operand(const uint32_t (&p)[8], int g) {
+template <int G>
+__device__ __forceinline__ bf16x8 p_operand(const uint32_t (&p)[4 * G], int g) {
   return __builtin_bit_cast(bf16x8, make_uint4(p[4 * g], p[4 * g + 1], p[4 * g + 2], p[4 * g + 3]));
 }
 
 // Phase u: S(u+1) = K(u+1) Q^T and O^T += V(u-1)^T P(u-1)^T on the MFMA pipe, while the VALU
 // turns S(u) into P(u) and l.  k_cur / v_cur hold K(u+1) and V(u-1); k_next holds K(u+2),
 // whose first kLead operands (those of the next phase) are read at the end of this one.
-// Element n of a unit is register n % 4 of accumulator n / 4 = g * 2 + kt.
-template <bool kMask, typename SlotHook>
-__device__ __forceinline__ void phase(WaveState& w, const f32x4 (&s_cur)[4], f32x4 (&s_next)[4],
-                                      const uint32_t (&p_prev)[8], uint32_t (&p_cur)[8],
+// Element n of a unit is register n % 4 of accumulator n / 4 = g * 2 + kt.  The unit's 8 G
+// softmax elements are spread over the 16 slots: one per slot for G = 2, one every other
+// slot for G = 1.
+template <bool kMask, int G, typename SlotHook>
+__device__ __forceinline__ void phase(WaveState<G>& w, const f32x4 (&s_cur)[2 * G], f32x4 (&s_next)[2 * G],
+                                      const uint32_t (&p_prev)[4 * G], uint32_t (&p_cur)[4 * G],
                                       const uint8_t* k_cur, const uint8_t* v_cur, const uint8_t* k_next,
                                       int key_base, int length, int h, SlotHook&& hook) {
-  f32x4 sv[4];
+  static_assert(G == 1 || G == 2, "one or two query groups per wave");
+  constexpr int E = 8 * G;   // softmax elements per lane per unit
+  f32x4 sv[2 * G];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < 2 * G; ++i) {
     sv[i] = s_cur[i];
     asm volatile("" : "+v"(sv[i]));
   }
-  float t[16], e[16];
+  float t[E], e[E];
   auto mul = [&](int n) { t[n] = sv[n >> 2][n & 3] * kLog2e; };
   auto ex = [&](int n) { e[n] = __builtin_amdgcn_exp2f(t[n]); };
   auto pack = [&](int n) {  // elements n, n+1 -> p_cur[n/2]
@@ -187,8 +198,9 @@ __device__ __forceinline__ void phase(WaveState& w, const f32x4 (&s_cur)[4], f32
     p_cur[n >> 1] = flk::pack_bf16x2(e0, e1);
     asm volatile("" : "+v"(p_cur[n >> 1]));   // keep the pack in its MFMA slot
   };
-  const bf16x8 pb0 = p_operand(p_prev, 0);
-  const bf16x8 pb1 = p_operand(p_prev, 1);
+  bf16x8 pb[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) pb[g] = p_operand<G>(p_prev, g);
 
   mul(0);
   mul(1);
@@ -200,23 +212,34 @@ __device__ __forceinline__ void phase(WaveState& w, const f32x4 (&s_cur)[4], f32
     if (n < 8) {
       const int st = n >> 1, kt = n & 1;
       // each S chain starts from the MFMA's inline zero accumulator
-      s_next[kt] = mfma16(a, w.qreg[st][0], st == 0 ? f32x4{} : s_next[kt]);
-      s_next[2 + kt] = mfma16(a, w.qreg[st][1], st == 0 ? f32x4{} : s_next[2 + kt]);
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+        s_next[2 * g + kt] = mfma16(a, w.qreg[st][g], st == 0 ? f32x4{} : s_next[2 * g + kt]);
     } else {
       const int dt = n - 8;
-      w.oacc[dt][0] = mfma16(a, pb0, w.oacc[dt][0]);
-      w.oacc[dt][1] = mfma16(a, pb1, w.oacc[dt][1]);
+#pragma unroll
+      for (int g = 0; g < G; ++g) w.oacc[dt][g] = mfma16(a, pb[g], w.oacc[dt][g]);
       if (dt == 7) {
-        w.lacc[0] = mfma16(w.ones, pb0, w.lacc[0]);
-        w.lacc[1] = mfma16(w.ones, pb1, w.lacc[1]);
+#pragma unroll
+        for (int g = 0; g < G; ++g) w.lacc[g] = mfma16(w.ones, pb[g], w.lacc[g]);
       }
     }
     const int nl = n + kLead;   // slot whose operand is read now
     if (nl < 16) w.ops[nl % kOpRing] = load_operand(w, nl, k_cur, v_cur);
     else w.ops[(nl - 16) % kOpRing] = load_operand(w, nl - 16, k_next, v_cur);
-    if (n + 2 < 16) mul(n + 2);
-    if (n + 1 < 16) ex(n + 1);
-    if (n & 1) pack(n - 1);
+    if constexpr (G == 2) {
+      if (n + 2 < E) mul(n + 2);
+      if (n + 1 < E) ex(n + 1);
+      if (n & 1) pack(n - 1);
+    } else {
+      const int m = n >> 1;
+      if ((n & 1) == 0) {
+        if (m + 1 < E) ex(m + 1);
+        if (m + 2 < E) mul(m + 2);
+      } else if (m & 1) {
+        pack(m - 1);
+      }
+    }
     hook(n);   // the iteration's tile copies, one instruction on some slots
     __builtin_amdgcn_sched_barrier(0);
   }
@@ -281,8 +304,8 @@ struct Ctx {
 // the iteration (1.3% faster at 4608 keys than the block of four, measured).
 constexpr int kDmaSlot[kDmaPerIter] = {1, 3, 17, 19};
 
-template <bool kMask>
-__device__ __forceinline__ void iteration(WaveState& w, const Ctx& c, int t, int r) {
+template <bool kMask, int G>
+__device__ __forceinline__ void iteration(WaveState<G>& w, const Ctx& c, int t, int r) {
   const TileCopy kc = plan_copy(c.smem + kKRing + ((r + 3) & 3) * kTileBytes, c.kh, t + 3, c.cp);
   const TileCopy vc = plan_copy(c.smem + kVRing + ((r + 2) & 3) * kTileBytes, c.vh, t + 2, c.cp);
   auto hook_a = [&](int n) {
@@ -307,21 +330,22 @@ __device__ __forceinline__ void iteration(WaveState& w, const Ctx& c, int t, int
   const uint8_t* v_tm1 = c.smem + kVRing + ((r + 3) & 3) * kTileBytes;   // V tile t-1
   const int key0 = t * kBN;
   // phase 2t: K(2t+1), V(2t-1), next K(2t+2); phase 2t+1: K(2t+2), V(2t), next K(2t+3)
-  phase<kMask>(w, w.sA, w.sB, w.pB, w.pA, k_t + kUnitBytes, v_tm1 + kUnitBytes, k_t1, key0, c.length, c.h, hook_a);
-  phase<kMask>(w, w.sB, w.sA, w.pA, w.pB, k_t1, v_t, k_t1 + kUnitBytes, key0 + 32, c.length, c.h, hook_b);
+  phase<kMask, G>(w, w.sA, w.sB, w.pB, w.pA, k_t + kUnitBytes, v_tm1 + kUnitBytes, k_t1, key0, c.length, c.h, hook_a);
+  phase<kMask, G>(w, w.sB, w.sA, w.pA, w.pB, k_t1, v_t, k_t1 + kUnitBytes, key0 + 32, c.length, c.h, hook_b);
   // Wait for the copies started one iteration ago, then a plain s_barrier: the LDS reads
   // still in flight touch no buffer the next copies write, so no lgkmcnt wait is needed.
   asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" :: "n"(kDmaPerIter) : "memory");
 }
 
-// One segment of work for a block: head bh (batch-major), query tile qblk, key tiles
-// [t_begin, t_end).  On return w holds the segment's unnormalised O^T accumulators and row
+// One segment of work for a block: head bh (batch-major), key tiles [t_begin, t_end), and
+// for this wave the 16 G queries from q0.  On return w holds the segment's unnormalised O^T accumulators and row
 // sums (lacc), and every LDS read and copy of the segment has completed.  Ring slots count from
 // the segment's first tile, so the unrolled loop keeps literal ring positions wherever the
 // range starts.
-__device__ __forceinline__ void attend_segment(WaveState& w, uint8_t* smem, const uint16_t* __restrict__ q,
+template <int G>
+__device__ __forceinline__ void attend_segment(WaveState<G>& w, uint8_t* smem, const uint16_t* __restrict__ q,
                                                const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
-                                               int length, int bh, int qblk, int t_begin, int t_end) {
+                                               int length, int bh, int q0, int t_begin, int t_end) {
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   Ctx c;
@@ -353,14 +377,13 @@ __device__ __forceinline__ void attend_segment(WaveState& w, uint8_t* smem, cons
   for (int tl = 0; tl < 3; ++tl) copy_tile(smem + kKRing + tl * kTileBytes, c.kh, t_begin + tl, c.cp);
   for (int tl = 0; tl < 2; ++tl) copy_tile(smem + kVRing + tl * kTileBytes, c.vh, t_begin + tl, c.cp);
 
-  const int q0 = qblk * kBM + wave * 32;   // query group g of this wave: q0 + 16 g .. + 15
   // k-slots 8h..8h+7 of the S MFMAs take d chunk dperm = 4 st + perm(h) of the K and Q rows,
   // perm(h) = 0, 2, 1, 3: lanes l and l + 32 then read neighbouring chunks (c, c ^ 1), which
   // the swizzle keeps on distinct banks whether a b128 read is served as 16 consecutive lanes
   // or as 8 lanes from each half of the wave.
   const int hperm = ((c.h & 1) << 1) | (c.h >> 1);
 #pragma unroll
-  for (int g = 0; g < 2; ++g) {
+  for (int g = 0; g < G; ++g) {   // query group g of this wave: q0 + 16 g .. + 15
     const int qi = q0 + g * 16 + col;
 #pragma unroll
     for (int st = 0; st < 4; ++st)
@@ -369,8 +392,11 @@ __device__ __forceinline__ void attend_segment(WaveState& w, uint8_t* smem, cons
                           : bf16x8{};
   }
 #pragma unroll
-  for (int dt = 0; dt < 8; ++dt) w.oacc[dt][0] = w.oacc[dt][1] = f32x4{};
-  w.lacc[0] = w.lacc[1] = f32x4{};
+  for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+    for (int g = 0; g < G; ++g) w.oacc[dt][g] = f32x4{};
+#pragma unroll
+  for (int g = 0; g < G; ++g) w.lacc[g] = f32x4{};
   {
     const __bf16 one = (lane & 15) == 0 ? (__bf16)1.0f : (__bf16)0.0f;
     w.ones = bf16x8{one, one, one, one, one, one, one, one};
@@ -397,7 +423,7 @@ __device__ __forceinline__ void attend_segment(WaveState& w, uint8_t* smem, cons
     }
   }
 #pragma unroll
-  for (int i = 0; i < 8; ++i) w.pB[i] = 0u;   // P(-1) = 0: phase 0's PV MFMAs add nothing
+  for (int i = 0; i < 4 * G; ++i) w.pB[i] = 0u;   // P(-1) = 0: phase 0's PV MFMAs add nothing
   // ... and the V(-1) operand they read (V ring slot 3, unit 1) is zeroed, so 0 * V = 0.
   reinterpret_cast<uint4*>(smem + kVRing + 3 * kTileBytes + kUnitBytes)[tid] = make_uint4(0, 0, 0, 0);
 
@@ -409,8 +435,8 @@ __device__ __forceinline__ void attend_segment(WaveState& w, uint8_t* smem, cons
   for (int n = 0; n < 8; ++n) {
     const int st = n >> 1, kt = n & 1;
     const bf16x8 a = load_operand(w, n, smem, smem);
-    w.sA[kt] = mfma16(a, w.qreg[st][0], st == 0 ? f32x4{} : w.sA[kt]);
-    w.sA[2 + kt] = mfma16(a, w.qreg[st][1], st == 0 ? f32x4{} : w.sA[2 + kt]);
+#pragma unroll
+    for (int g = 0; g < G; ++g) w.sA[2 * g + kt] = mfma16(a, w.qreg[st][g], st == 0 ? f32x4{} : w.sA[2 * g + kt]);
   }
 #pragma unroll
   for (int n = 0; n < kLead; ++n) w.ops[n % kOpRing] = load_operand(w, n, smem + kUnitBytes, smem);
@@ -420,49 +446,51 @@ __device__ __forceinline__ void attend_segment(WaveState& w, uint8_t* smem, cons
   const int full_end = min(length / kBN, t_end);
   int t = t_begin;
   for (; t + 4 <= full_end; t += 4) {
-    iteration<false>(w, c, t, 0);
-    iteration<false>(w, c, t + 1, 1);
-    iteration<false>(w, c, t + 2, 2);
-    iteration<false>(w, c, t + 3, 3);
+    iteration<false, G>(w, c, t, 0);
+    iteration<false, G>(w, c, t + 1, 1);
+    iteration<false, G>(w, c, t + 2, 2);
+    iteration<false, G>(w, c, t + 3, 3);
   }
-  for (; t < t_end; ++t) iteration<true>(w, c, t, (t - t_begin) & 3);
+  for (; t < t_end; ++t) iteration<true, G>(w, c, t, (t - t_begin) & 3);
   // No copy may still be writing this block's LDS when the segment ends.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   // Drain: O^T += V(U-1)^T P(U-1)^T for the last unit (unit 1 of the last tile).
   {
     const uint8_t* v_last = smem + kVRing + ((t_end - 1 - t_begin) & 3) * kTileBytes + kUnitBytes;
-    const bf16x8 pb0 = p_operand(w.pB, 0);
-    const bf16x8 pb1 = p_operand(w.pB, 1);
+    bf16x8 pb[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) pb[g] = p_operand<G>(w.pB, g);
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
       const bf16x8 a = load_operand(w, 8 + dt, v_last, v_last);
-      w.oacc[dt][0] = mfma16(a, pb0, w.oacc[dt][0]);
-      w.oacc[dt][1] = mfma16(a, pb1, w.oacc[dt][1]);
+#pragma unroll
+      for (int g = 0; g < G; ++g) w.oacc[dt][g] = mfma16(a, pb[g], w.oacc[dt][g]);
     }
-    w.lacc[0] = mfma16(w.ones, pb0, w.lacc[0]);
-    w.lacc[1] = mfma16(w.ones, pb1, w.lacc[1]);
+#pragma unroll
+    for (int g = 0; g < G; ++g) w.lacc[g] = mfma16(w.ones, pb[g], w.lacc[g]);
   }
 }
 
 // l of each query group from lanes 0-15 (row 0 of the row-sum tile) to the lanes of every
 // lane group.
-__device__ __forceinline__ void row_sums(const WaveState& w, float (&l)[2]) {
+template <int G>
+__device__ __forceinline__ void row_sums(const WaveState<G>& w, float (&l)[G]) {
   const int lane = threadIdx.x & 63;
 #pragma unroll
-  for (int g = 0; g < 2; ++g) l[g] = __shfl(w.lacc[g][0], lane & 15);
+  for (int g = 0; g < G; ++g) l[g] = __shfl(w.lacc[g][0], lane & 15);
 }
 
-// O = bf16(acc / l) of the wave's 32 queries, 4 d values per 8-byte store.
-__device__ __forceinline__ void store_o(const WaveState& w, const float (&l)[2], uint16_t* __restrict__ o, int bh,
-                                        int heads, int qblk, int length, int64_t o_batch_stride,
+// O = bf16(acc / l) of the wave's 16 G queries from q0, 4 d values per 8-byte store.
+template <int G>
+__device__ __forceinline__ void store_o(const WaveState<G>& w, const float (&l)[G], uint16_t* __restrict__ o, int bh,
+                                        int heads, int q0, int length, int64_t o_batch_stride,
                                         int64_t o_head_stride, int64_t o_row_stride) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
   const int h4 = lane >> 4, col = lane & 15;
-  const int q0 = qblk * kBM + wave * 32;
   const int b = bh / heads, hd = bh - b * heads;
 #pragma unroll
-  for (int g = 0; g < 2; ++g) {
+  for (int g = 0; g < G; ++g) {
     const int qi = q0 + g * 16 + col;
     if (qi >= length) continue;
     uint16_t* orow = o + b * o_batch_stride + hd * o_head_stride + (int64_t)qi * o_row_stride;
@@ -485,7 +513,7 @@ __device__ __forceinline__ void store_o(const WaveState& w, const float (&l)[2],
 // is coherent across the device on its own, so a reader on any CU that loads it the same
 // way after the writer's stores have completed sees it; no cache-wide write-back needed).
 template <bool kCoherent = false>
-__device__ __forceinline__ void store_partial(const WaveState& w, const float (&l)[2], float* __restrict__ part_acc,
+__device__ __forceinline__ void store_partial(const WaveState<2>& w, const float (&l)[2], float* __restrict__ part_acc,
                                               float* __restrict__ part_l, int64_t slot) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t ws = slot * kWaves + wave;
@@ -544,15 +572,52 @@ __global__ __launch_bounds__(kThreads, 2) void attend_kernel(
     t_end = (split + 1) * ntiles / splits;
   }
 
-  WaveState w;
-  attend_segment(w, smem, q, k, v, length, bh, qblk, t_begin, t_end);
+  const int q0 = qblk * kBM + (threadIdx.x >> 6) * 32;   // this wave's 32 queries
+  WaveState<2> w;
+  attend_segment(w, smem, q, k, v, length, bh, q0, t_begin, t_end);
   float l[2];
   row_sums(w, l);
   if constexpr (kSplit) {
     const int64_t units = total_blocks / splits;
     store_partial(w, l, part_acc, part_l, (int64_t)split * units + (int64_t)bh * q_blocks + qblk);
   } else {
-    store_o(w, l, o, bh, heads, qblk, length, o_batch_stride, o_head_stride, o_row_stride);
+    store_o(w, l, o, bh, heads, q0, length, o_batch_stride, o_head_stride, o_row_stride);
+  }
+}
+
+// The same with 192-query tiles, for grids that fit the CUs in one round either way: waves
+// 0-3 take 32 queries each (two groups) and waves 4-7 16 each (one group), so every SIMD
+// still holds one wave of each kind and 48 queries instead of 64.  Every query's arithmetic
+// is attend_kernel's, so the output is the same, bit for bit.
+constexpr int kBM192 = 192;
+
+__global__ __launch_bounds__(kThreads, 2) void attend_tile192_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+    uint16_t* __restrict__ o, int length, int q_blocks, int total_blocks, int heads, int64_t o_batch_stride,
+    int64_t o_head_stride, int64_t o_row_stride) {
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[kSmemBytes];
+  const int p = blockIdx.x;
+  const int xcd = p % kXcds, local = p / kXcds;
+  const int per = total_blocks / kXcds, extra = total_blocks % kXcds;
+  const int logical = xcd * per + min(xcd, extra) + local;
+  const int qblk = logical % q_blocks;
+  const int bh = logical / q_blocks;
+  const int ntiles = (length + kBN - 1) / kBN;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform branch below
+  if (wave < 4) {
+    const int q0 = qblk * kBM192 + wave * 32;
+    WaveState<2> w;
+    attend_segment(w, smem, q, k, v, length, bh, q0, 0, ntiles);
+    float l[2];
+    row_sums(w, l);
+    store_o(w, l, o, bh, heads, q0, length, o_batch_stride, o_head_stride, o_row_stride);
+  } else {
+    const int q0 = qblk * kBM192 + 128 + (wave - 4) * 16;
+    WaveState<1> w;
+    attend_segment(w, smem, q, k, v, length, bh, q0, 0, ntiles);
+    float l[1];
+    row_sums(w, l);
+    store_o(w, l, o, bh, heads, q0, length, o_batch_stride, o_head_stride, o_row_stride);
   }
 }
 
@@ -656,14 +721,15 @@ __global__ __launch_bounds__(kThreads, 2) void attend_balanced_kernel(
     }
     const int bh = unit / q_blocks, qblk = unit - bh * q_blocks;
     __syncthreads();   // every wave is done with the previous segment's LDS
-    WaveState w;
-    attend_segment(w, smem, q, k, v, length, bh, qblk, t0, t1);
+    const int q0 = qblk * kBM + (threadIdx.x >> 6) * 32;
+    WaveState<2> w;
+    attend_segment(w, smem, q, k, v, length, bh, q0, t0, t1);
     float ls[2];
     row_sums(w, ls);
     const int cf = i < 0 ? 0 : range_of(xs, i * ntiles);
     const int cl = i < 0 ? 0 : range_of(xs, (i + 1) * ntiles - 1);
     if (cf == cl) {   // a whole tile of one range
-      store_o(w, ls, o, bh, heads, qblk, length, o_batch_stride, o_head_stride, o_row_stride);
+      store_o(w, ls, o, bh, heads, q0, length, o_batch_stride, o_head_stride, o_row_stride);
       continue;
     }
     const int others = cl - cf, pos = l - cf;
@@ -690,7 +756,7 @@ __global__ __launch_bounds__(kThreads, 2) void attend_balanced_kernel(
     } else {
       for (int c = cf; c <= cl; ++c) gather_partial(w.oacc, ls, c == cf, part_acc, part_l, slot_of(c));
     }
-    store_o(w, ls, o, bh, heads, qblk, length, o_batch_stride, o_head_stride, o_row_stride);
+    store_o(w, ls, o, bh, heads, q0, length, o_batch_stride, o_head_stride, o_row_stride);
     if (threadIdx.x == 0) *counter = 0;
   }
 }
@@ -771,8 +837,26 @@ int64_t split_workspace_bytes(int batch, int heads, int length, int splits) {
   return (int64_t)splits * batch * heads * q_tiles(length) * kThreads * 65 * (int64_t)sizeof(float);
 }
 
+// 192-query tiles when the grid fits the CUs in one round with them as with 256-query tiles:
+// the launch then takes the time of one block, and a 192-query block does 3/4 of the work.
+int64_t q_tiles192(int length) { return (length + kBM192 - 1) / kBM192; }
+
+bool tile192_preferred(int batch, int heads, int length) {
+  const int64_t bh = (int64_t)batch * heads;
+  return q_tiles(length) * bh <= kCUs && q_tiles192(length) * bh <= kCUs;
+}
+
 int launch_attend(const void* q, const void* k, const void* v, void* o, int batch, int heads, int length,
                   int64_t o_batch_stride, int64_t o_head_stride, int64_t o_row_stride, void* stream) {
+  if (tile192_preferred(batch, heads, length)) {
+    const int64_t total = q_tiles192(length) * batch * heads;
+    hipLaunchKernelGGL(attend_tile192_kernel, dim3((unsigned)total), dim3(kThreads), 0,
+                       static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(q),
+                       static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
+                       static_cast<uint16_t*>(o), length, (int)q_tiles192(length), (int)total, heads,
+                       o_batch_stride, o_head_stride, o_row_stride);
+    return flk_launch_status();
+  }
   const int64_t total = q_tiles(length) * batch * heads;
   hipLaunchKernelGGL(attend_kernel<false>, dim3((unsigned)total), dim3(kThreads), 0,
                      static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(q),

@@ -79,7 +79,8 @@ int flk_qk_prep_ids(const void* qkv, int64_t qkv_batch_stride, int64_t qkv_row_s
  * Replaces kernels.attend (src/flicker/kernels.py:105-145).
  *   q, k, v, o (batch, heads, length, head_dim) bf16, contiguous; q is already scaled by
  *   1/sqrt(head_dim).  o = bf16(sum_j bf16(exp(q.k_j)) v_j / sum_j f32(bf16(exp(q.k_j)))).
- * Any length >= 1 (tail tiles are masked).  head_dim must be 128.
+ * Any length >= 1 (tail tiles are masked).  head_dim must be 128.  The query tile size
+ * (256, or 192 when both fit the GPU's CUs in one round) does not change the result.
  */
 int flk_attend(const void* q, const void* k, const void* v, void* o,
                int batch, int heads, int length, int head_dim, void* stream);

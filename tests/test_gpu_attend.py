@@ -65,6 +65,21 @@ def test_attend_matches_bounded_oracle(device, batch, heads, length):
     tight_gate(f"B{batch} H{heads} L{length}", got, want)
 
 
+@pytest.mark.parametrize("heads,length", [(24, 1536), (5, 1000), (3, 4608), (2, 193)])
+def test_attend_192_query_tiles_equal_256_query_tiles(device, heads, length):
+    """A grid that fits the 256 CUs in one round with 192-query tiles as with 256-query ones
+    runs the 192-query kernel (waves of two and of one 16-query group); every query's
+    arithmetic is the 256-query kernel's, so the output is the same bit for bit.  The same
+    heads repeated over a batch with more than 256 tiles of 256 queries run that kernel."""
+    q, k, v = prepped_case(1, heads, length, seed=40 + length)
+    small = run_attend(q, k, v, device, splits=1)
+    reps = 256 // (heads * -(-length // 256)) + 1
+    big = run_attend(*(t.expand(reps, -1, -1, -1) for t in (q, k, v)), device, splits=1)
+    for b in range(reps):
+        assert np.array_equal(big[b].view(np.uint32), small[0].view(np.uint32)), b
+    tight_gate(f"192-query tiles H{heads} L{length}", small, P.attend_bounded(to_np(q), to_np(k), to_np(v)))
+
+
 def test_attend_peaked_logits(device):
     """Large norm scales (bound 11.3 * 2.4^2 = 65 < 80): far-from-uniform attention."""
     q, k, v = prepped_case(1, 2, 512, seed=5, scale=2.4)
