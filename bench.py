@@ -85,6 +85,12 @@ def traffic_file(workload: str) -> str:
     return os.path.join(ROOT, "profiles", f"hbm_traffic_{workload}.json")
 
 
+def _is_attend(kernel_name: str) -> bool:
+    """Any of attend's one-pass kernels (256- or 192-query tiles, rounds, balanced, key split),
+    not the split path's merge."""
+    return "attend_" in kernel_name and "_kernel" in kernel_name and "merge" not in kernel_name
+
+
 def _counter_means(directory: str, counter: str) -> dict:
     files = glob.glob(os.path.join(directory, "**", "*counter_collection.csv"), recursive=True)
     if not files:
@@ -95,7 +101,7 @@ def _counter_means(directory: str, counter: str) -> dict:
             if row["Counter_Name"] != counter:
                 continue
             name = row["Kernel_Name"]
-            key = ("attend" if "attend_kernel" in name else "qk_prep" if "qk_prep_kernel" in name
+            key = ("attend" if _is_attend(name) else "qk_prep" if "qk_prep_kernel" in name
                    else "w8a8_gemm" if "w8a8_gemm_kernel<false, false" in name
                    else "copy" if ("copyBuffer" in name or "copy" in name.lower()) else None)
             if key:
@@ -127,7 +133,7 @@ def ingest_mfma(directory: str, workload: str, last: int = 20) -> dict:
     for f in files:
         for row in csv.DictReader(open(f)):
             name = row["Kernel_Name"]
-            key = ("attend" if "attend_kernel" in name else
+            key = ("attend" if _is_attend(name) else
                    "w8a8_gemm" if "w8a8_gemm_kernel<false, false" in name else None)
             if key:
                 d = rows.setdefault(key, {}).setdefault(int(row["Dispatch_Id"]), {})
@@ -579,7 +585,8 @@ def main() -> int:
         "roofline": {"bound": "mfma", "achieved": round(at_tflops, 2), "peak": BF16_DENSE_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(at_tflops / BF16_DENSE_PEAK_TFLOPS, 4),
                      "traffic": round(traffic["attend"]["traffic_bytes"]) if traffic else None,
-                     "traffic_source": source, "kernel": "attend_kernel",
+                     "traffic_source": source,
+                     "kernel": " + ".join(kernels.attend_kernels(w.batch, w.num_heads, w.length)),
                      "flops_per_launch": w.attend_flops(), "avg_launch_us": round(at_ms * 1e3, 2),
                      "p50_launch_us": at_p50,
                      **mfma_fields("attend")},

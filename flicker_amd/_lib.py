@@ -32,6 +32,7 @@ SIGNATURES = {
     "flk_attend_balanced_to": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _i64, _i64, _i64, _p, _i64, _p]),
     "flk_attend_balanced_plan": (_i, [_i, _i, _i, _ip, ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int64)]),
     "flk_attend_plan": (_i, [_i, _i, _i, _ip, ctypes.POINTER(ctypes.c_int64)]),
+    "flk_attend_kernel": (ctypes.c_char_p, [_i, _i, _i]),
     "flk_rope_embed": (_i, [_p, _i64, _i64, _i, _ip, _f, _p, _p]),
     "flk_lane_pair": (_i, [_p, _i64, _i, _p, _p, _p]),
     "flk_rope_lanes": (_i, [_p, _i64, _i64, _i, _ip, _f, _p, _p, _p]),
@@ -137,6 +138,12 @@ def attend_plan(batch: int, heads: int, length: int) -> tuple[int, int]:
     check(lib().flk_attend_plan(batch, heads, length, ctypes.byref(splits), ctypes.byref(nbytes)),
           "flk_attend_plan")
     return splits.value, nbytes.value
+
+
+@functools.lru_cache(maxsize=1024)
+def attend_kernel_name(batch: int, heads: int, length: int) -> str:
+    """Name of the kernel flk_attend / flk_attend_to launch for this shape."""
+    return lib().flk_attend_kernel(batch, heads, length).decode()
 
 
 @functools.lru_cache(maxsize=1024)

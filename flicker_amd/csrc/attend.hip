@@ -591,6 +591,32 @@ __global__ __launch_bounds__(kThreads, 2) void attend_kernel(
 // is attend_kernel's, so the output is the same, bit for bit.
 constexpr int kBM192 = 192;
 
+// One block of 256 queries from q_start (every wave two query groups) or, with tile192, of
+// 192 (waves 4-7 one group each); queries at or past q_limit (<= length) are not stored.
+__device__ __forceinline__ void query_tile(uint8_t* smem, const uint16_t* __restrict__ q,
+                                           const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+                                           uint16_t* __restrict__ o, int length, int bh, int q_start, int q_limit,
+                                           bool tile192, int heads, int64_t o_batch_stride, int64_t o_head_stride,
+                                           int64_t o_row_stride) {
+  const int ntiles = (length + kBN - 1) / kBN;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform branch below
+  if (!tile192 || wave < 4) {
+    const int q0 = q_start + wave * 32;
+    WaveState<2> w;
+    attend_segment(w, smem, q, k, v, length, bh, q0, 0, ntiles);
+    float l[2];
+    row_sums(w, l);
+    store_o(w, l, o, bh, heads, q0, q_limit, o_batch_stride, o_head_stride, o_row_stride);
+  } else {
+    const int q0 = q_start + 128 + (wave - 4) * 16;
+    WaveState<1> w;
+    attend_segment(w, smem, q, k, v, length, bh, q0, 0, ntiles);
+    float l[1];
+    row_sums(w, l);
+    store_o(w, l, o, bh, heads, q0, q_limit, o_batch_stride, o_head_stride, o_row_stride);
+  }
+}
+
 __global__ __launch_bounds__(kThreads, 2) void attend_tile192_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     uint16_t* __restrict__ o, int length, int q_blocks, int total_blocks, int heads, int64_t o_batch_stride,
@@ -602,23 +628,57 @@ __global__ __launch_bounds__(kThreads, 2) void attend_tile192_kernel(
   const int logical = xcd * per + min(xcd, extra) + local;
   const int qblk = logical % q_blocks;
   const int bh = logical / q_blocks;
-  const int ntiles = (length + kBN - 1) / kBN;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform branch below
-  if (wave < 4) {
-    const int q0 = qblk * kBM192 + wave * 32;
-    WaveState<2> w;
-    attend_segment(w, smem, q, k, v, length, bh, q0, 0, ntiles);
-    float l[2];
-    row_sums(w, l);
-    store_o(w, l, o, bh, heads, q0, length, o_batch_stride, o_head_stride, o_row_stride);
-  } else {
-    const int q0 = qblk * kBM192 + 128 + (wave - 4) * 16;
-    WaveState<1> w;
-    attend_segment(w, smem, q, k, v, length, bh, q0, 0, ntiles);
-    float l[1];
-    row_sums(w, l);
-    store_o(w, l, o, bh, heads, q0, length, o_batch_stride, o_head_stride, o_row_stride);
+  query_tile(smem, q, k, v, o, length, bh, qblk * kBM192, length, true, heads, o_batch_stride, o_head_stride,
+             o_row_stride);
+}
+
+// Rounds launch, for grids of more than one round: each XCD takes a contiguous range of the
+// 256-query tiles (b, h, tile), as the balanced launch deals them, runs whole rounds of 32
+// of them, and cuts the queries of the tiles left over into 192-query tiles, head by head,
+// so that the last round has up to 4/3 as many blocks with 3/4 of the work each.
+
+// The j-th 192-query tile of the queries of 256-query tiles [first, end): head segment by
+// head segment, the last tile of a segment cut short at its end (q_end).  False past the last.
+__device__ __forceinline__ bool leftover_tile(int first, int end, int q_blocks, int length, int j, int& bh,
+                                              int& q_start, int& q_end) {
+  for (int u = first; u < end;) {
+    const int b = u / q_blocks, t0 = u - b * q_blocks;
+    const int t1 = min(q_blocks, t0 + (end - u));
+    const int s = t0 * kBM, e = min(t1 * kBM, length);
+    const int count = (e - s + kBM192 - 1) / kBM192;
+    if (j < count) {
+      bh = b;
+      q_start = s + j * kBM192;
+      q_end = min(q_start + kBM192, e);
+      return true;
+    }
+    j -= count;
+    u += t1 - t0;
   }
+  return false;
+}
+
+__global__ __launch_bounds__(kThreads, 2) void attend_rounds_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+    uint16_t* __restrict__ o, int length, int q_blocks, int units, int heads, int64_t o_batch_stride,
+    int64_t o_head_stride, int64_t o_row_stride) {
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[kSmemBytes];
+  constexpr int C = kCUs / kXcds;
+  const int x = blockIdx.x % kXcds, l = blockIdx.x / kXcds;   // hardware deals blocks round-robin over XCDs
+  const int ux0 = (int)((int64_t)x * units / kXcds);
+  const int n = (int)((int64_t)(x + 1) * units / kXcds) - ux0;
+  const int full = n / C * C;
+  if (l < full) {
+    const int unit = ux0 + l;
+    const int bh = unit / q_blocks, qblk = unit - bh * q_blocks;
+    query_tile(smem, q, k, v, o, length, bh, qblk * kBM, length, false, heads, o_batch_stride, o_head_stride,
+               o_row_stride);
+    return;
+  }
+  int bh, q_start, q_end;
+  if (!leftover_tile(ux0 + full, ux0 + n, q_blocks, length, l - full, bh, q_start, q_end)) return;
+  query_tile(smem, q, k, v, o, length, bh, q_start, q_end, true, heads, o_batch_stride, o_head_stride,
+             o_row_stride);
 }
 
 // Balanced attend: one persistent block per CU (256), so that the last, partial round of
@@ -846,8 +906,43 @@ bool tile192_preferred(int batch, int heads, int length) {
   return q_tiles(length) * bh <= kCUs && q_tiles192(length) * bh <= kCUs;
 }
 
+// Grid of the rounds launch (attend_rounds_kernel), or 0 when it is not the choice: it needs
+// a full round of 256-query tiles on every XCD, tiles left over, and at most one round (32
+// per XCD) of 192-query tiles for them.
+int64_t rounds_grid(int batch, int heads, int length) {
+  constexpr int C = kCUs / kXcds;
+  const int64_t units = q_tiles(length) * batch * heads;
+  if (units < kCUs || units > INT32_MAX) return 0;
+  const int64_t qb = q_tiles(length);
+  int64_t most = 0, left_max = 0;
+  for (int x = 0; x < kXcds; ++x) {
+    const int64_t ux0 = x * units / kXcds, n = (x + 1) * units / kXcds - ux0;
+    const int64_t full = n / C * C;
+    int64_t count = 0;
+    for (int64_t u = ux0 + full; u < ux0 + n;) {   // as leftover_tile walks them
+      const int64_t b = u / qb, t0 = u - b * qb, t1 = std::min(qb, t0 + (ux0 + n - u));
+      const int64_t e = std::min<int64_t>(t1 * kBM, length);
+      count += (e - t0 * kBM + kBM192 - 1) / kBM192;
+      u += t1 - t0;
+    }
+    if (count > C) return 0;
+    left_max = std::max(left_max, n - full);
+    most = std::max(most, full + count);
+  }
+  return left_max > 0 ? most * kXcds : 0;
+}
+
 int launch_attend(const void* q, const void* k, const void* v, void* o, int batch, int heads, int length,
                   int64_t o_batch_stride, int64_t o_head_stride, int64_t o_row_stride, void* stream) {
+  if (const int64_t grid = rounds_grid(batch, heads, length)) {
+    hipLaunchKernelGGL(attend_rounds_kernel, dim3((unsigned)grid), dim3(kThreads), 0,
+                       static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(q),
+                       static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
+                       static_cast<uint16_t*>(o), length, (int)q_tiles(length),
+                       (int)(q_tiles(length) * batch * heads), heads, o_batch_stride, o_head_stride,
+                       o_row_stride);
+    return flk_launch_status();
+  }
   if (tile192_preferred(batch, heads, length)) {
     const int64_t total = q_tiles192(length) * batch * heads;
     hipLaunchKernelGGL(attend_tile192_kernel, dim3((unsigned)total), dim3(kThreads), 0,
@@ -867,6 +962,13 @@ int launch_attend(const void* q, const void* k, const void* v, void* o, int batc
 }
 
 }  // namespace
+
+extern "C" const char* flk_attend_kernel(int batch, int heads, int length) {
+  if (batch <= 0 || heads <= 0 || length <= 0) return "";
+  if (rounds_grid(batch, heads, length)) return "attend_rounds_kernel";
+  if (tile192_preferred(batch, heads, length)) return "attend_tile192_kernel";
+  return "attend_kernel";
+}
 
 extern "C" int flk_attend(const void* q, const void* k, const void* v, void* o, int batch,
                           int heads, int length, int head_dim, void* stream) {
@@ -896,19 +998,19 @@ constexpr int64_t kSlotLBytes = (int64_t)kWaves * 64 * 4;
 int64_t balanced_counters_offset(int grid) { return 2 * (int64_t)grid * (kSlotAccBytes + kSlotLBytes); }
 int64_t balanced_workspace_bytes(int grid) { return balanced_counters_offset(grid) + 4 * (int64_t)grid; }
 
-// Whether the balanced launch beats one block per tile, by the tiles an XCD has left after
-// its full rounds of 32: it does when every XCD has at least one full round and the last
-// round would leave more than 3/8 of the CUs idle (measured: 11% at 64 or 88 of 256 CUs
-// busy, 7-9% at 48, 2.5% at 152), and not at 176 of 256 (a plain last round on fewer CUs
-// runs at a higher clock under the power limit, which makes up for the idle CUs, and each
-// shared tile's hand-off costs several microseconds) nor with no full round (144 tiles:
-// 45-49 us against 39 us).
+// Whether the balanced launch beats the rounds launch (one block per 256-query tile, the
+// tiles an XCD has left after its full rounds of 32 re-tiled by 192 queries), by those
+// leftover tiles of the fullest XCD: it does when every XCD has at least one full round, at
+// most 16 tiles are left over and each CU's share of their keys is at least 16 key tiles
+// (measured against the rounds launch: 6% at 8 left over, 2-5% at 11-12, 1% at 13; the
+// rounds launch 2% faster at 19 left over, and 20% at 4 left over of 24 key tiles each,
+// whose shares of 3 key tiles spend more on hand-offs than on keys).
 bool balanced_preferred(int batch, int heads, int length) {
   const int64_t units = q_tiles(length) * batch * heads;
   constexpr int C = kCUs / kXcds;
   if (units < kCUs || units > INT32_MAX || (int64_t)(length + kBN - 1) / kBN * 1024 > INT32_MAX) return false;
   const int64_t left = ((units + kXcds - 1) / kXcds) % C;   // leftover tiles of the fullest XCD
-  return left > 0 && left * 8 <= C * 5;
+  return left > 0 && left <= 16 && left * ((length + kBN - 1) / kBN) >= 16 * C;
 }
 
 }  // namespace

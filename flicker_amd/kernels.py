@@ -283,6 +283,17 @@ def attend_merged(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
     return out
 
 
+def attend_kernels(batch: int, heads: int, length: int) -> tuple[str, ...]:
+    """Names of the kernels ``attend`` launches for a (batch, heads, length, 128) problem, in
+    order, as kernel traces show them (for profiling; the choice is _launch_attend's)."""
+    splits, _ = _lib.attend_plan(batch, heads, length)
+    if splits > 1:
+        return ("attend_kernel<true>", "attend_merge_kernel")
+    if _lib.attend_balanced_plan(batch, heads, length)[0] > 0:
+        return ("attend_balanced_kernel",)
+    return (_lib.attend_kernel_name(batch, heads, length),)
+
+
 def _launch_attend(q, k, v, out, o_strides, splits: int | None, balanced: bool | None = None) -> None:
     """O through strides (batch, head, row): with ``splits`` None the plan's choice -- the
     key-split path when the grid is small, the balanced path (flk_attend_balanced_to: one

@@ -79,11 +79,21 @@ int flk_qk_prep_ids(const void* qkv, int64_t qkv_batch_stride, int64_t qkv_row_s
  * Replaces kernels.attend (src/flicker/kernels.py:105-145).
  *   q, k, v, o (batch, heads, length, head_dim) bf16, contiguous; q is already scaled by
  *   1/sqrt(head_dim).  o = bf16(sum_j bf16(exp(q.k_j)) v_j / sum_j f32(bf16(exp(q.k_j)))).
- * Any length >= 1 (tail tiles are masked).  head_dim must be 128.  The query tile size
- * (256, or 192 when both fit the GPU's CUs in one round) does not change the result.
+ * Any length >= 1 (tail tiles are masked).  head_dim must be 128.  How queries are tiled
+ * (flk_attend_kernel) does not change the result.
  */
 int flk_attend(const void* q, const void* k, const void* v, void* o,
                int batch, int heads, int length, int head_dim, void* stream);
+
+/*
+ * Name of the kernel flk_attend / flk_attend_to launch for this shape (no counterpart in the
+ * reference; for profilers and benchmarks, which match kernel traces by name):
+ * "attend_kernel" (one block per 256-query tile), "attend_tile192_kernel" (192-query tiles:
+ * grids that fit the 256 CUs in one round either way) or "attend_rounds_kernel" (whole
+ * rounds of 256-query tiles per XCD, the tiles left over re-tiled by 192 queries); "" for an
+ * empty shape.  The three give the same output bits.
+ */
+const char* flk_attend_kernel(int batch, int heads, int length);
 
 /*
  * flk_attend writing O through strides (elements): o[b, h, t, :] starts at

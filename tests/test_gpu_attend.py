@@ -80,6 +80,25 @@ def test_attend_192_query_tiles_equal_256_query_tiles(device, heads, length):
     tight_gate(f"192-query tiles H{heads} L{length}", small, P.attend_bounded(to_np(q), to_np(k), to_np(v)))
 
 
+@pytest.mark.parametrize("batch,heads,length", [(1, 24, 4608), (1, 24, 4352), (1, 48, 1536), (3, 7, 4100)])
+def test_attend_rounds_launch_equals_one_head_at_a_time(device, batch, heads, length):
+    """Grids of more than one round run whole rounds of 256-query tiles per XCD and re-tile
+    the queries of the tiles left over by 192 (leftover head segments that start mid-head,
+    tiles cut short at a segment's end).  Each query's arithmetic is unchanged, so every head
+    equals the same head launched alone (a one-round grid), bit for bit; two heads are also
+    held to the bounded oracle."""
+    q, k, v = prepped_case(batch, heads, length, seed=50 + length)
+    got = run_attend(q, k, v, device, splits=1)
+    for b in range(batch):
+        for h in range(heads):
+            one = run_attend(*(t[b:b + 1, h:h + 1] for t in (q, k, v)), device, splits=1)
+            assert np.array_equal(got[b:b + 1, h:h + 1].view(np.uint32), one.view(np.uint32)), (b, h)
+    for b, h in ((0, 0), (batch - 1, heads - 1)):
+        sl = (slice(b, b + 1), slice(h, h + 1))
+        tight_gate(f"rounds B{batch} H{heads} L{length} head {b},{h}", got[sl],
+                   P.attend_bounded(*(to_np(t[sl]) for t in (q, k, v))))
+
+
 def test_attend_peaked_logits(device):
     """Large norm scales (bound 11.3 * 2.4^2 = 65 < 80): far-from-uniform attention."""
     q, k, v = prepped_case(1, 2, 512, seed=5, scale=2.4)

@@ -102,13 +102,15 @@ def test_attend_split_plan_and_validation(lib):
 
 def test_attend_balanced_plan_and_validation(lib):
     """flk_attend_balanced_plan prefers the balanced launch only where every XCD has a full
-    round of 32 tiles and the fullest XCD's last round would be at most 5/8 full (Klein
-    1024^2: 54 tiles per XCD, 22 left over -> one block per tile; 2048^2: 198 -> 6 left over
-    -> balanced; 512^2: 18 -> one block per tile); its workspace does not depend on the
-    shape.  flk_attend_balanced_to rejects short or misaligned workspaces before launching
-    anything."""
+    round of 32 tiles, at most 16 are left over on the fullest XCD, and each CU's share of
+    their keys is at least 16 key tiles (Klein 1024^2: 54 tiles per XCD, 22 left over -> the
+    rounds launch; 2048^2: 198 -> 6 left over -> balanced; 1536x640: 19 left over -> rounds;
+    48 heads at 1536 tokens: 4 left over, shares of 3 key tiles -> rounds; 512^2: 18 tiles,
+    no full round); its workspace does not depend on the shape.  flk_attend_balanced_to
+    rejects short or misaligned workspaces before launching anything."""
     ws = 2 * 256 * (8 * 1024 * 16 + 8 * 64 * 4)
-    cases = {(1, 24, 4608): 0, (4, 24, 4608): 0, (1, 24, 16896): 256, (1, 24, 4352): 256, (1, 32, 4608): 256,
+    cases = {(1, 24, 4608): 0, (4, 24, 4608): 0, (1, 24, 16896): 256, (1, 24, 4352): 0, (1, 32, 4608): 256,
+             (2, 24, 4608): 256, (3, 7, 4100): 256, (1, 48, 1536): 0,
              (1, 24, 6400): 256, (1, 128, 512): 0, (1, 6, 4608): 0, (1, 24, 1536): 0, (1, 40, 1000): 0,
              (0, 3, 4608): 0}
     for (b, h, length), want in cases.items():
@@ -127,6 +129,19 @@ def test_attend_balanced_plan_and_validation(lib):
     with pytest.raises(_lib.HipKernelError):
         _lib.check(lib.flk_attend_balanced_plan(1, -1, 10, ctypes.byref(ctypes.c_int()), ctypes.byref(ctypes.c_int64()),
                                                 ctypes.byref(ctypes.c_int64())), "flk_attend_balanced_plan")
+
+
+def test_attend_kernel_names(lib):
+    """flk_attend_kernel names what flk_attend launches: 192-query tiles where both tilings fit
+    the 256 CUs in one round, whole rounds plus 192-query leftovers where every XCD has a full
+    round and its leftover tiles fit one round of 192-query tiles, else one block per tile."""
+    cases = {(1, 24, 1536): "attend_tile192_kernel", (1, 3, 4608): "attend_tile192_kernel",
+             (1, 1, 1): "attend_tile192_kernel", (1, 24, 4608): "attend_rounds_kernel",
+             (1, 24, 4352): "attend_rounds_kernel", (1, 48, 1536): "attend_rounds_kernel",
+             (1, 128, 512): "attend_kernel", (1, 64, 1024): "attend_kernel", (0, 24, 4608): "",
+             (1, 24, 0): ""}
+    for shape, want in cases.items():
+        assert _lib.attend_kernel_name(*shape) == want, (shape, _lib.attend_kernel_name(*shape))
 
 
 def test_attend_split_static_validation(lib):
