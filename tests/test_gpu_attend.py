@@ -145,7 +145,7 @@ def test_attend_python_api_errors(device):
         kernels.attend(q, k, v, interpret=True)
 
 
-@pytest.mark.parametrize("batch,heads,length", [(1, 3, 100), (2, 2, 257), (1, 24, 1536)])
+@pytest.mark.parametrize("batch,heads,length", [(1, 3, 100), (2, 2, 257), (1, 24, 1536), (1, 24, 4608), (1, 48, 1536)])
 def test_attend_merged_equals_merge_heads_of_attend(device, batch, heads, length):
     """The token-major epilogue (flk_attend_to) writes exactly merge_heads(attend(q, k, v))
     (modules.py:63-65): same kernel, different store address -> bit-identical."""

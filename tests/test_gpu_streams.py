@@ -91,6 +91,42 @@ def test_graph_replay_qk_prep_attend(device):
         assert torch.equal(replayed, eager), f"replay with input seed {seed} differs from eager"
 
 
+def test_graph_replay_attend_rounds(device):
+    """The rounds launch (whole rounds of 256-query tiles, the leftover re-tiled by 192) keeps
+    no state between calls, so a captured attend replays exactly: the Klein 1024^2 shape."""
+    from flicker_amd import _lib
+    heads, length = 24, 4608
+    assert _lib.attend_kernel_name(1, heads, length) == "attend_rounds_kernel"
+
+    def inputs(seed):
+        g = torch.Generator().manual_seed(seed)
+        x = torch.randn(3, 1, heads, length, D, generator=g)
+        x[:2] = x[:2] / x[:2].pow(2).mean(-1, keepdim=True).sqrt()
+        x[0] = x[0] / math.sqrt(D)
+        return [t.to(torch.bfloat16).to(device) for t in x]
+
+    static = inputs(20)
+    static_o = torch.empty_like(static[0])
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        kernels.attend(*static, out=static_o)      # warm-up outside the capture
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        kernels.attend(*static, out=static_o)
+    for seed in (21, 22, 23):
+        fresh = inputs(seed)
+        for dst, src in zip(static, fresh):
+            dst.copy_(src)
+        graph.replay()
+        torch.cuda.synchronize()
+        replayed = static_o.clone()
+        eager = kernels.attend(*fresh)                # eager work between replays
+        torch.cuda.synchronize()
+        assert torch.equal(replayed, eager), f"replay with input seed {seed} differs from eager"
+
+
 def test_graph_replay_int8_projection(device):
     proj = workloads.Projection("t", 512, 384, 3 * 2 * D)
     x0, w = workloads.make_projection(proj)
