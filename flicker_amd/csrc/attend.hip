@@ -585,11 +585,7 @@ __global__ __launch_bounds__(kThreads, 2) void attend_kernel(
   }
 }
 
-// The same with 192-query tiles, for grids that fit the CUs in one round either way: waves
-// 0-3 take 32 queries each (two groups) and waves 4-7 16 each (one group), so every SIMD
-// still holds one wave of each kind and 48 queries instead of 64.  Every query's arithmetic
-// is attend_kernel's, so the output is the same, bit for bit.
-constexpr int kBM192 = 192;
+constexpr int kBM192 = 192;   // queries per block of the 192-query tiles
 
 // One block of 256 queries from q_start (every wave two query groups) or, with tile192, of
 // 192 (waves 4-7 one group each); queries at or past q_limit (<= length) are not stored.
@@ -617,6 +613,10 @@ __device__ __forceinline__ void query_tile(uint8_t* smem, const uint16_t* __rest
   }
 }
 
+// attend_kernel<false> with 192-query tiles, for grids that fit the CUs in one round either
+// way: waves 0-3 take 32 queries each (two groups) and waves 4-7 16 each (one group), so
+// every SIMD still holds one wave of each kind and 48 queries instead of 64.  Every query's
+// arithmetic is attend_kernel's, so the output is the same, bit for bit.
 __global__ __launch_bounds__(kThreads, 2) void attend_tile192_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     uint16_t* __restrict__ o, int length, int q_blocks, int total_blocks, int heads, int64_t o_batch_stride,
