@@ -37,6 +37,12 @@
 // share an XCD (and its L2), and grouped so that 4 token tiles sweep the channel tiles
 // together.
 //
+// A one-problem launch of more than one round (the Klein projection: 648 tiles, 2.53 rounds
+// of 256 CUs) takes the rounds order: each XCD runs whole rounds of 32 of its tiles, then
+// cuts the tiles left over into tiles of 192 tokens (waves of 128 x 48: three token
+// fragments), so the partial last round has up to 4/3 as many blocks with 3/4 of the work
+// each (measured 1-5% faster for the plain GEMM, 3-6% with the qk_prep epilogue).
+//
 // A launch takes up to two problems (GemmGroup; the activation quantiser likewise takes a
 // QuantGroup): a double block's text and image projections share one grid, so the small
 // text projection runs on the CUs the image projection leaves idle in its last round.
@@ -380,10 +386,9 @@ constexpr int kGStage = 2 * kGHalf;      // WqT rows, then Xq rows; two stages f
 constexpr int kGWaves = 8;               // two waves per SIMD
 constexpr int kGThreads = kGWaves * 64;
 constexpr int kGWaveN = 128;             // a wave's output channels (8 fragments of 16)
-constexpr int kGWaveM = 64;              // a wave's tokens (4 fragments of 16)
 constexpr int kGNF = kGWaveN / 16;       // channel fragments per wave
-constexpr int kGMF = kGWaveM / 16;       // token fragments per wave
-constexpr int kGCopies = kGT / kGWaves / 8;   // copy instructions per operand per wave and stage (4)
+constexpr int kGCopies = kGT / kGWaves / 8;   // WqT copy instructions per wave and stage (4)
+constexpr int kGT192 = 192;              // token edge of the tiles that re-tile a partial last round
 constexpr int kGRing = 4;                // channel-fragment registers in flight
 constexpr int kGLead = 3;                // groups between a channel fragment's read and its MFMAs
 static_assert(kGNF % kGRing == 0 && kGRing > kGLead, "the fragment ring must divide the groups of a step");
@@ -392,6 +397,7 @@ static_assert(kGNF % kGRing == 0 && kGRing > kGLead, "the fragment ring must div
 #endif
 constexpr int kGroup = FLK_GEMM_GROUP;   // token tiles that sweep the channel tiles together
 constexpr int kXcds = 8;
+constexpr int kCUs = 256;                // MI355X compute units
 
 // LDS slot of 16-byte chunk c in row r is c ^ gswz(r).  gfx950's LDS serves 256 B per clock
 // from 64 banks, i.e. two 128-byte operand rows; a b128 read is served as lanes 0-7 with
@@ -404,31 +410,9 @@ __device__ __forceinline__ int gswz(int row) { return (row & 7) ^ ((row >> 3) & 
 __device__ __forceinline__ const uint8_t* a_frag(const uint8_t* stage, int nf, int wn) {
   return stage + (wn * kGWaveN + nf * 16) * kGK;
 }
+template <int kWaveM>
 __device__ __forceinline__ const uint8_t* b_frag(const uint8_t* stage, int mf, int wm) {
-  return stage + kGHalf + (wm * kGWaveM + mf * 16) * kGK;
-}
-
-// One 64-byte k step of the wave's 128 x 64 sub-tile: 8 groups of 4 MFMAs, group nf on the
-// channel fragment in ring[nf % 4] and the 4 token fragments in b_cur.  Group nf reads the
-// channel fragment of group nf + 3 (of this step, or the next step's first three from
-// `a_next` at offset `off_next`) and, when b_from <= nf < b_from + 4, one token fragment of
-// the next step into b_nxt.
-template <int kBFrom>
-__device__ __forceinline__ void gemm_step(i32x4 (&acc)[kGNF][kGMF], i32x4 (&ring)[kGRing], const i32x4 (&b_cur)[kGMF],
-                                          i32x4 (&b_nxt)[kGMF], const uint8_t* a_src, int off, const uint8_t* a_next,
-                                          const uint8_t* b_next, int off_next, int wn, int wm) {
-#pragma unroll
-  for (int nf = 0; nf < kGNF; ++nf) {
-#pragma unroll
-    for (int mf = 0; mf < kGMF; ++mf)
-      acc[nf][mf] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ring[nf % kGRing], b_cur[mf], acc[nf][mf], 0, 0, 0);
-    const int nl = nf + kGLead;
-    if (nl < kGNF) ring[nl % kGRing] = *reinterpret_cast<const i32x4*>(a_frag(a_src, nl, wn) + off);
-    else ring[nl % kGRing] = *reinterpret_cast<const i32x4*>(a_frag(a_next, nl - kGNF, wn) + off_next);
-    if (nf >= kBFrom && nf < kBFrom + kGMF)
-      b_nxt[nf - kBFrom] = *reinterpret_cast<const i32x4*>(b_frag(b_next, nf - kBFrom, wm) + off_next);
-    __builtin_amdgcn_sched_barrier(0);
-  }
+  return stage + kGHalf + (wm * kWaveM + mf * 16) * kGK;
 }
 
 // The fused epilogue's qk_prep parameters (see flk_w8a8_qk_prep): output row m of the
@@ -465,27 +449,21 @@ struct GemmProblem {
 struct GemmGroup {
   GemmProblem p[2];
   int first_blocks;
+  int rounds;   // one problem, rounds order (w8a8_gemm_kernel)
 };
 
 // kAcc: also write the exact int32 products (a test and debugging path).
 // kQk: instead of Y, run qk_prep on each finished bf16 head row (kScaleF32: float32 norm
 // scales) and write head-major q, k, v.
-template <bool kAcc, bool kQk = false, bool kScaleF32 = false>
-__global__ __launch_bounds__(kGThreads, 2) void w8a8_gemm_kernel(const GemmGroup grp) {
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * kGStage];
+// One output tile: channels n0 .. n0 + 255 and tokens m0 .. m0 + 64 kMF - 1 (kMF = 4: 256
+// tokens; 3: 192), of which tokens below m_limit are stored.  Each of the 2 (channels) x 4
+// (tokens) waves holds 128 channels x 16 kMF tokens.
+template <bool kAcc, bool kQk, bool kScaleF32, int kMF>
+__device__ __forceinline__ void gemm_tile(uint8_t* smem, const GemmProblem& P, int m0, int n0, int m_limit) {
+  constexpr int kWaveM = 16 * kMF;   // a wave's tokens
+  constexpr int kBCopies = kMF;      // Xq copy instructions per wave and stage (8 kMF rows)
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-
-  // Tile order: blocks are dealt round-robin over the XCDs; renumber so that each XCD runs
-  // a contiguous range of logical tiles (of one problem, then the next), then walk kGroup
-  // token tiles across all channel tiles before moving on.
-  const int nblocks = gridDim.x;
-  const int xcd = blockIdx.x % kXcds, local = blockIdx.x / kXcds;
-  const int per = nblocks / kXcds, extra = nblocks % kXcds;
-  const int logical_all = xcd * per + min(xcd, extra) + local;
-  const bool second = logical_all >= grp.first_blocks;
-  const GemmProblem& P = second ? grp.p[1] : grp.p[0];   // wave-uniform, read from the kernel arguments
-  const int logical = logical_all - (second ? grp.first_blocks : 0);
   const int8_t* __restrict__ xq = P.xq;
   const int8_t* __restrict__ wqt = P.wqt;
   const float* __restrict__ a_scale = P.a_scale;
@@ -493,31 +471,29 @@ __global__ __launch_bounds__(kGThreads, 2) void w8a8_gemm_kernel(const GemmGroup
   uint16_t* __restrict__ y = P.y;
   const int64_t y_stride = P.y_stride;
   int32_t* __restrict__ acc_out = P.acc_out;
-  const int M = P.M, K = P.K, N = P.N, tiles_m = P.tiles_m, tiles_n = P.tiles_n;
+  const int M = P.M, K = P.K, N = P.N;
   const QkEpilogue& qe = P.qe;
-  const int group_tiles = kGroup * tiles_n;
-  const int group = logical / group_tiles;
-  const int first_m = group * kGroup;
-  const int gm = min(kGroup, tiles_m - first_m);
-  const int in_group = logical - group * group_tiles;
-  const int m0 = (first_m + in_group % gm) * kGT;
-  const int n0 = (in_group / gm) * kGT;
 
-  // Copy sources: this wave fills rows wave*32 .. +31 of both operands, 8 rows (64 lanes x
-  // 16 B) per instruction; lane i lands at row i/8, slot i%8, and fetches chunk slot^gswz.
+  // Copy sources: this wave fills rows wave*32 .. +31 of WqT and wave*8kMF .. +8kMF-1 of Xq,
+  // 8 rows (64 lanes x 16 B) per instruction; lane i lands at row i/8, slot i%8, and fetches
+  // chunk slot^gswz.
   // Rows past the matrix edge repeat the last row (their results are never stored).  The
   // tile's first row (plus the stage's k offset) is a scalar base; lanes add 32-bit offsets.
   const int8_t* abase = wqt + (int64_t)n0 * K;
   const int8_t* bbase = xq + (int64_t)m0 * K;
-  uint32_t aoff[kGCopies], boff[kGCopies];
+  uint32_t aoff[kGCopies], boff[kBCopies];
 #pragma unroll
   for (int i = 0; i < kGCopies; ++i) {
     const int row = wave * (kGT / kGWaves) + i * 8 + (lane >> 3);
-    const uint32_t chunk = (uint32_t)(((lane & 7) ^ gswz(row)) * 16);
-    aoff[i] = (uint32_t)min(row, N - 1 - n0) * (uint32_t)K + chunk;
-    boff[i] = (uint32_t)min(row, M - 1 - m0) * (uint32_t)K + chunk;
+    aoff[i] = (uint32_t)min(row, N - 1 - n0) * (uint32_t)K + (uint32_t)(((lane & 7) ^ gswz(row)) * 16);
   }
-  uint8_t* const wave_lds = smem + wave * (kGT / kGWaves) * kGK;   // this wave's copy rows in stage 0
+#pragma unroll
+  for (int i = 0; i < kBCopies; ++i) {
+    const int row = wave * 8 * kMF + i * 8 + (lane >> 3);
+    boff[i] = (uint32_t)min(row, M - 1 - m0) * (uint32_t)K + (uint32_t)(((lane & 7) ^ gswz(row)) * 16);
+  }
+  uint8_t* const a_lds = smem + wave * (kGT / kGWaves) * kGK;   // this wave's WqT rows in stage 0
+  uint8_t* const b_lds = smem + kGHalf + wave * 8 * kMF * kGK;  // ... and its Xq rows
 
   const int KT = K / kGK;
   const int wn = wave >> 2, wm = wave & 3;     // 2 (channels) x 4 (tokens) waves
@@ -527,11 +503,11 @@ __global__ __launch_bounds__(kGThreads, 2) void w8a8_gemm_kernel(const GemmGroup
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) off[ks] = l16 * kGK + (((4 * ks + hperm) ^ gswz(l16)) * 16);
 
-  i32x4 acc[kGNF][kGMF];
+  i32x4 acc[kGNF][kMF];
 #pragma unroll
   for (int a = 0; a < kGNF; ++a)
 #pragma unroll
-    for (int b = 0; b < kGMF; ++b) acc[a][b] = i32x4{};
+    for (int b = 0; b < kMF; ++b) acc[a][b] = i32x4{};
 
   // Two stages of 128 k bytes, two 64-byte k steps each.  Stage kt: step 0 reads step 1's
   // fragments as it goes; step 1 reads its own last channel fragments in groups 0-4, then --
@@ -540,31 +516,30 @@ __global__ __launch_bounds__(kGThreads, 2) void w8a8_gemm_kernel(const GemmGroup
   // Past the last stage the copies repeat it (into the buffer no later step reads), so
   // every stage issues the same copies and vmcnt(0) is exact.
   const int k1 = min(1, KT - 1) * kGK;
+  auto copy_stage = [&](int k_off, int buf) {   // WqT and Xq copies alternating
 #pragma unroll
-  for (int i = 0; i < kGCopies; ++i) {
-    flk::dma16_at(abase, aoff[i], wave_lds + i * 8 * kGK);
-    flk::dma16_at(bbase, boff[i], wave_lds + kGHalf + i * 8 * kGK);
-  }
-#pragma unroll
-  for (int i = 0; i < kGCopies; ++i) {
-    flk::dma16_at(abase + k1, aoff[i], wave_lds + kGStage + i * 8 * kGK);
-    flk::dma16_at(bbase + k1, boff[i], wave_lds + kGStage + kGHalf + i * 8 * kGK);
-  }
-  asm volatile("s_waitcnt vmcnt(%0)" :: "n"(2 * kGCopies) : "memory");   // stage 0 landed
+    for (int i = 0; i < kGCopies; ++i) {
+      flk::dma16_at(abase + k_off, aoff[i], a_lds + buf * kGStage + i * 8 * kGK);
+      if (i < kBCopies) flk::dma16_at(bbase + k_off, boff[i], b_lds + buf * kGStage + i * 8 * kGK);
+    }
+  };
+  copy_stage(0, 0);
+  copy_stage(k1, 1);
+  asm volatile("s_waitcnt vmcnt(%0)" :: "n"(kGCopies + kBCopies) : "memory");   // stage 0 landed
   __syncthreads();
-  i32x4 ring[kGRing], b0[kGMF], b1[kGMF];
+  i32x4 ring[kGRing], b0[kMF], b1[kMF];
 #pragma unroll
-  for (int mf = 0; mf < kGMF; ++mf) b0[mf] = *reinterpret_cast<const i32x4*>(b_frag(smem, mf, wm) + off[0]);
+  for (int mf = 0; mf < kMF; ++mf) b0[mf] = *reinterpret_cast<const i32x4*>(b_frag<kWaveM>(smem, mf, wm) + off[0]);
 #pragma unroll
   for (int nf = 0; nf < kGLead; ++nf) ring[nf] = *reinterpret_cast<const i32x4*>(a_frag(smem, nf, wn) + off[0]);
 
-  auto mfma_group = [&](int nf, const i32x4 (&b)[kGMF]) {
+  auto mfma_group = [&](int nf, const i32x4 (&b)[kMF]) {
 #pragma unroll
-    for (int mf = 0; mf < kGMF; ++mf)
+    for (int mf = 0; mf < kMF; ++mf)
       acc[nf][mf] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ring[nf % kGRing], b[mf], acc[nf][mf], 0, 0, 0);
   };
   auto afrag = [&](const uint8_t* st, int nf, int o) { return *reinterpret_cast<const i32x4*>(a_frag(st, nf, wn) + o); };
-  auto bfrag = [&](const uint8_t* st, int mf, int o) { return *reinterpret_cast<const i32x4*>(b_frag(st, mf, wm) + o); };
+  auto bfrag = [&](const uint8_t* st, int mf, int o) { return *reinterpret_cast<const i32x4*>(b_frag<kWaveM>(st, mf, wm) + o); };
 
   for (int kt = 0; kt < KT; ++kt) {
     const uint8_t* cs = smem + (kt & 1) * kGStage;          // stage kt
@@ -576,7 +551,7 @@ __global__ __launch_bounds__(kGThreads, 2) void w8a8_gemm_kernel(const GemmGroup
       mfma_group(nf, b0);
       const int nl = nf + kGLead;
       ring[nl % kGRing] = nl < kGNF ? afrag(cs, nl, off[0]) : afrag(cs, nl - kGNF, off[1]);
-      if (nf < kGMF) b1[nf] = bfrag(cs, nf, off[1]);
+      if (nf < kMF) b1[nf] = bfrag(cs, nf, off[1]);
       __builtin_amdgcn_sched_barrier(0);
     }
     // step 1, groups reading stage kt
@@ -587,22 +562,22 @@ __global__ __launch_bounds__(kGThreads, 2) void w8a8_gemm_kernel(const GemmGroup
       __builtin_amdgcn_sched_barrier(0);
     }
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");   // stage kt read, kt+1 landed
-#pragma unroll
-    for (int i = 0; i < kGCopies; ++i) {
-      flk::dma16_at(abase + k_next, aoff[i], wave_lds + (kt & 1) * kGStage + i * 8 * kGK);
-      flk::dma16_at(bbase + k_next, boff[i], wave_lds + (kt & 1) * kGStage + kGHalf + i * 8 * kGK);
-    }
+    copy_stage(k_next, kt & 1);
     // step 1, groups reading stage kt+1 (its step 0 fragments)
 #pragma unroll
     for (int nf = kGNF - kGLead; nf < kGNF; ++nf) {
       mfma_group(nf, b1);
       ring[(nf + kGLead) % kGRing] = afrag(ns, nf + kGLead - kGNF, off[0]);
-      const int j = nf - (kGNF - kGLead);           // 0, 1, 2: token fragments 0-1, 2, 3
-      if (j == 0) {
-        b0[0] = bfrag(ns, 0, off[0]);
-        b0[1] = bfrag(ns, 1, off[0]);
-      } else {
-        b0[j + 1] = bfrag(ns, j + 1, off[0]);
+      const int j = nf - (kGNF - kGLead);           // 0, 1, 2
+      if constexpr (kMF == 4) {                     // token fragments 0-1, 2, 3
+        if (j == 0) {
+          b0[0] = bfrag(ns, 0, off[0]);
+          b0[1] = bfrag(ns, 1, off[0]);
+        } else {
+          b0[j + 1] = bfrag(ns, j + 1, off[0]);
+        }
+      } else {                                      // token fragments 0, 1, 2
+        b0[j] = bfrag(ns, j, off[0]);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -616,9 +591,9 @@ __global__ __launch_bounds__(kGThreads, 2) void w8a8_gemm_kernel(const GemmGroup
     for (int nf = 0; nf < kGNF; ++nf) {
       const int n = n0 + wn * kGWaveN + nf * 16 + h4 * 4;
 #pragma unroll
-      for (int mf = 0; mf < kGMF; ++mf) {
-        const int m = m0 + wm * kGWaveM + mf * 16 + l16;
-        if (n < N && m < M) *reinterpret_cast<i32x4*>(acc_out + (int64_t)m * N + n) = acc[nf][mf];
+      for (int mf = 0; mf < kMF; ++mf) {
+        const int m = m0 + wm * kWaveM + mf * 16 + l16;
+        if (n < N && m < m_limit) *reinterpret_cast<i32x4*>(acc_out + (int64_t)m * N + n) = acc[nf][mf];
       }
     }
   }
@@ -629,17 +604,17 @@ __global__ __launch_bounds__(kGThreads, 2) void w8a8_gemm_kernel(const GemmGroup
   // the wave reads back 4 rows per instruction (16 lanes x 16 B per row) and writes each
   // row's 256 contiguous bytes with 16-byte nontemporal stores (Y is streamed out: 1-2%
   // faster, and a qk_prep pass reading Y next measured no slower).
-  float am[kGMF];
+  float am[kMF];
 #pragma unroll
-  for (int mf = 0; mf < kGMF; ++mf) am[mf] = a_scale[min(m0 + wm * kGWaveM + mf * 16 + l16, M - 1)];
+  for (int mf = 0; mf < kMF; ++mf) am[mf] = a_scale[min(m0 + wm * kWaveM + mf * 16 + l16, M - 1)];
   __syncthreads();   // every wave is done reading the operand stages
-  uint8_t* const out_lds = smem + wave * (kGWaveM * 256);
+  uint8_t* const out_lds = smem + wave * (kWaveM * 256);
 #pragma unroll
   for (int nf = 0; nf < kGNF; ++nf) {
     // w_o of the lane's 4 channels (clamped at the edge; clamped values are never stored)
     const f32x4 w4 = *reinterpret_cast<const f32x4*>(w_scale + min(n0 + wn * kGWaveN + nf * 16 + h4 * 4, N - 4));
 #pragma unroll
-    for (int mf = 0; mf < kGMF; ++mf) {
+    for (int mf = 0; mf < kMF; ++mf) {
       const int ml = mf * 16 + l16;
       const float y0 = ((float)acc[nf][mf][0] * am[mf]) * w4.x;
       const float y1 = ((float)acc[nf][mf][1] * am[mf]) * w4.y;
@@ -654,7 +629,7 @@ __global__ __launch_bounds__(kGThreads, 2) void w8a8_gemm_kernel(const GemmGroup
   }
   // Each wave reads back only what it wrote itself: its LDS writes complete in order before
   // its reads (the compiler waits on lgkmcnt), so no barrier is needed here.
-  constexpr int kReads = kGWaveM / 4;
+  constexpr int kReads = kWaveM / 4;
   const int n_lane = n0 + wn * kGWaveN + (lane & 15) * 8;
   if constexpr (kQk) {
     // The wave's 128 channels are one head of the q|k|v thirds (N = 3 H 128, tiles 128-aligned);
@@ -672,12 +647,12 @@ __global__ __launch_bounds__(kGThreads, 2) void w8a8_gemm_kernel(const GemmGroup
     // sequences divide per row).  A division per row measured 2.4% of the fused kernel.
     const int len = qe.length;
     const bool short_seq = len < 4;
-    const int m_first = m0 + wm * kGWaveM + (lane >> 4);
+    const int m_first = m0 + wm * kWaveM + (lane >> 4);
     int b = m_first / len, t = m_first - b * len;
 #pragma unroll 4
     for (int it = 0; it < kReads; ++it) {
       const int ml = it * 4 + (lane >> 4);
-      const int m = m0 + wm * kGWaveM + ml;
+      const int m = m0 + wm * kWaveM + ml;
       if (it > 0) {
         if (short_seq) {
           b = m / len;
@@ -691,7 +666,7 @@ __global__ __launch_bounds__(kGThreads, 2) void w8a8_gemm_kernel(const GemmGroup
         }
       }
       const uint4 v = *reinterpret_cast<const uint4*>(out_lds + ml * 256 + ((l16 ^ (ml & 15)) * 16));
-      if (m >= M) continue;   // uniform over the 16-lane row, so the DPP rows stay whole
+      if (m >= m_limit) continue;   // uniform over the 16-lane row, so the DPP rows stay whole
       uint4 r = v;
       if (sec < 2) {
         float c[8], s[8];
@@ -710,8 +685,8 @@ __global__ __launch_bounds__(kGThreads, 2) void w8a8_gemm_kernel(const GemmGroup
   for (int it = 0; it < kReads; ++it) {
     const int ml = it * 4 + (lane >> 4);
     const uint4 v = *reinterpret_cast<const uint4*>(out_lds + ml * 256 + (((lane & 15) ^ (ml & 15)) * 16));
-    const int m = m0 + wm * kGWaveM + ml;
-    if (m < M && n_lane < N) {
+    const int m = m0 + wm * kWaveM + ml;
+    if (m < m_limit && n_lane < N) {
       uint16_t* dst = y + (int64_t)m * y_stride + n_lane;
       if (wide && n_lane + 8 <= N) {
         __builtin_nontemporal_store(u32x4{v.x, v.y, v.z, v.w}, reinterpret_cast<u32x4*>(dst));
@@ -721,6 +696,86 @@ __global__ __launch_bounds__(kGThreads, 2) void w8a8_gemm_kernel(const GemmGroup
       }
     }
   }
+}
+
+// Logical tile u of a problem -> its token and channel tiles: kGroup token tiles sweep the
+// channel tiles together (consecutive logical tiles share a channel tile's WqT rows).
+__device__ __forceinline__ void tile_of(int u, int tiles_m, int tiles_n, int& mt, int& nt) {
+  const int group_tiles = kGroup * tiles_n;
+  const int group = u / group_tiles;
+  const int first_m = group * kGroup;
+  const int gm = min(kGroup, tiles_m - first_m);
+  const int in_group = u - group * group_tiles;
+  mt = first_m + in_group % gm;
+  nt = in_group / gm;
+}
+
+// The rounds order's 192-token tiles: logical tiles [first, end) taken as runs of one channel
+// tile (consecutive token tiles of one group), each run's tokens cut into 192-token tiles, the
+// last one short.  The j-th such tile, or false past the last.  The host's
+// gemm_rounds_grid counts them the same way.
+__device__ __forceinline__ bool leftover_tile(int first, int end, int tiles_m, int tiles_n, int M, int j, int& m0,
+                                              int& n0, int& m_end) {
+  for (int u = first; u < end;) {
+    const int group_tiles = kGroup * tiles_n;
+    const int group = u / group_tiles;
+    const int first_m = group * kGroup;
+    const int gm = min(kGroup, tiles_m - first_m);
+    const int in_group = u - group * group_tiles;
+    const int r = in_group % gm;
+    const int run = min(gm - r, end - u);
+    const int s = (first_m + r) * kGT, e = min((first_m + r + run) * kGT, M);
+    const int count = (e - s + kGT192 - 1) / kGT192;
+    if (j < count) {
+      m0 = s + j * kGT192;
+      m_end = min(m0 + kGT192, e);
+      n0 = (in_group / gm) * kGT;
+      return true;
+    }
+    j -= count;
+    u += run;
+  }
+  return false;
+}
+
+// kAcc: also write the exact int32 products (a test and debugging path).
+// kQk: instead of Y, run qk_prep on each finished bf16 head row (kScaleF32: float32 norm
+// scales) and write head-major q, k, v.
+template <bool kAcc, bool kQk = false, bool kScaleF32 = false>
+__global__ __launch_bounds__(kGThreads, 2) void w8a8_gemm_kernel(const GemmGroup grp) {
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * kGStage];
+  const int xcd = blockIdx.x % kXcds, local = blockIdx.x / kXcds;   // blocks are dealt round-robin over XCDs
+  if (grp.rounds) {
+    // Rounds order (one problem): each XCD takes a contiguous range of the logical tiles, runs
+    // whole rounds of 32 of them, and cuts the ones left over into 192-token tiles, so the
+    // partial last round has up to 4/3 as many blocks with 3/4 of the work each.
+    constexpr int C = kCUs / kXcds;
+    const GemmProblem& P = grp.p[0];
+    const int units = P.tiles_m * P.tiles_n;
+    const int ux0 = (int)((int64_t)xcd * units / kXcds);
+    const int n = (int)((int64_t)(xcd + 1) * units / kXcds) - ux0;
+    const int full = n / C * C;
+    if (local < full) {
+      int mt, nt;
+      tile_of(ux0 + local, P.tiles_m, P.tiles_n, mt, nt);
+      gemm_tile<kAcc, kQk, kScaleF32, 4>(smem, P, mt * kGT, nt * kGT, P.M);
+      return;
+    }
+    int m0, n0, m_end;
+    if (!leftover_tile(ux0 + full, ux0 + n, P.tiles_m, P.tiles_n, P.M, local - full, m0, n0, m_end)) return;
+    gemm_tile<kAcc, kQk, kScaleF32, 3>(smem, P, m0, n0, m_end);
+    return;
+  }
+  // Tile order: renumber so that each XCD runs a contiguous range of logical tiles (of one
+  // problem, then the next).
+  const int nblocks = gridDim.x;
+  const int per = nblocks / kXcds, extra = nblocks % kXcds;
+  const int logical_all = xcd * per + min(xcd, extra) + local;
+  const bool second = logical_all >= grp.first_blocks;
+  const GemmProblem& P = second ? grp.p[1] : grp.p[0];   // wave-uniform, read from the kernel arguments
+  int mt, nt;
+  tile_of(logical_all - (second ? grp.first_blocks : 0), P.tiles_m, P.tiles_n, mt, nt);
+  gemm_tile<kAcc, kQk, kScaleF32, 4>(smem, P, mt * kGT, nt * kGT, P.M);
 }
 
 inline hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
@@ -888,6 +943,35 @@ namespace {
 
 int64_t problem_blocks(const GemmProblem& p) { return (int64_t)p.tiles_m * p.tiles_n; }
 
+// Grid of the rounds order of one problem (w8a8_gemm_kernel), or 0 when it is not the choice:
+// it needs a full round of 32 tiles on every XCD, tiles left over, and at most one round of
+// 192-token tiles for them (counted as leftover_tile walks them).
+int64_t gemm_rounds_grid(const GemmProblem& p) {
+  constexpr int C = kCUs / kXcds;
+  const int64_t units = problem_blocks(p);
+  if (units < kCUs || units > INT32_MAX) return 0;
+  int64_t most = 0, left_max = 0;
+  for (int x = 0; x < kXcds; ++x) {
+    const int64_t ux0 = x * units / kXcds, n = (x + 1) * units / kXcds - ux0;
+    const int64_t full = n / C * C;
+    int64_t count = 0;
+    for (int64_t u = ux0 + full; u < ux0 + n;) {
+      const int64_t group_tiles = (int64_t)kGroup * p.tiles_n;
+      const int64_t group = u / group_tiles, first_m = group * kGroup;
+      const int64_t gm = std::min<int64_t>(kGroup, p.tiles_m - first_m);
+      const int64_t r = (u - group * group_tiles) % gm;
+      const int64_t run = std::min(gm - r, ux0 + n - u);
+      const int64_t e = std::min<int64_t>((first_m + r + run) * kGT, p.M);
+      count += (e - (first_m + r) * kGT + kGT192 - 1) / kGT192;
+      u += run;
+    }
+    if (count > C) return 0;
+    left_max = std::max(left_max, n - full);
+    most = std::max(most, full + count);
+  }
+  return left_max > 0 ? most * kXcds : 0;
+}
+
 template <bool kAcc, bool kQk, bool kScaleF32>
 int launch_group(const GemmGroup& g, int64_t blocks, void* stream) {
   if (blocks > INT32_MAX) return FLK_E_INVALID;
@@ -969,8 +1053,10 @@ extern "C" int flk_w8a8_gemm(const int8_t* xq, const int8_t* wq_t, const float* 
   p.tiles_m = (m + kGT - 1) / kGT;
   p.tiles_n = (n + kGT - 1) / kGT;
   g.p[1] = p;
-  const int64_t blocks = problem_blocks(p);
-  g.first_blocks = (int)std::min<int64_t>(blocks, INT32_MAX);
+  const int64_t rounds = gemm_rounds_grid(p);
+  const int64_t blocks = rounds ? rounds : problem_blocks(p);
+  g.first_blocks = (int)std::min<int64_t>(problem_blocks(p), INT32_MAX);
+  g.rounds = rounds > 0;
   return acc_or_null ? launch_group<true, false, false>(g, blocks, stream)
                      : launch_group<false, false, false>(g, blocks, stream);
 }
@@ -985,8 +1071,10 @@ extern "C" int flk_w8a8_qk_prep(const int8_t* xq, const int8_t* wq_t, const floa
                             batch, length, num_heads, head_dim, q_out, k_out, v_out, out_length, out_offset, g.p[0]);
   if (st != FLK_OK) return st == kNoWork ? FLK_OK : st;
   g.p[1] = g.p[0];
-  const int64_t blocks = problem_blocks(g.p[0]);
-  g.first_blocks = (int)std::min<int64_t>(blocks, INT32_MAX);
+  const int64_t rounds = gemm_rounds_grid(g.p[0]);
+  const int64_t blocks = rounds ? rounds : problem_blocks(g.p[0]);
+  g.first_blocks = (int)std::min<int64_t>(problem_blocks(g.p[0]), INT32_MAX);
+  g.rounds = rounds > 0;
   return launch_qk(g, blocks, scale_is_f32, stream);
 }
 

@@ -151,8 +151,29 @@ def test_quantize_act_near_ties(device):
                                    (4608, 3072, 9216 // 36), (2600, 384, 6000)])
 def test_gemm_tails_bit_exact(device, m, k, n):
     """Ragged tiles in both output dimensions; full-range int8 operands.  The last case has
-    11 x 24 = 264 tiles, more than one per CU, so blocks walk several tiles, ragged ones included."""
+    11 x 24 = 264 tiles, more than one round of 256 CUs: the rounds order runs 256 of them
+    whole and cuts the queries of the rest into 192-token tiles, ragged ones included."""
     rng = np.random.default_rng(m * 7 + n)
+    xq = rng.integers(-127, 128, (m, k), dtype=np.int8)
+    wq = rng.integers(-127, 128, (k, n), dtype=np.int8)
+    a = (rng.random(m, dtype=np.float32) * 0.05 + 1e-3).astype(np.float32)
+    ws = (rng.random(n, dtype=np.float32) * 0.002 + 1e-5).astype(np.float32)
+    acc = torch.empty((m, n), dtype=torch.int32, device=device)
+    y = w8a8.gemm(torch.from_numpy(xq).to(device), torch.from_numpy(a).to(device),
+                  torch.from_numpy(np.ascontiguousarray(wq.T)).to(device), torch.from_numpy(ws).to(device), acc=acc)
+    acc_want = Q.int_gemm(xq, wq)
+    np.testing.assert_array_equal(host(acc), acc_want)
+    assert_bits_equal(y, Q.rescale(acc_want, a, ws), f"y {m}x{k}x{n}")
+
+
+@pytest.mark.parametrize("m,n", [(4352, 9216), (3840, 9216), (4100, 9000), (2600, 9216), (6000, 6144)])
+def test_gemm_rounds_order_bit_exact(device, m, n):
+    """Grids of more than one round (the Klein QKV widths): whole rounds of 256 x 256 tiles,
+    then the tiles left over cut into 192-token tiles, runs of one channel tile starting and
+    ending between token tiles, the last tile of a run cut short.  Every int32 product and
+    bf16 output against the oracle (K = 128 keeps the float64 oracle product quick)."""
+    k = 128
+    rng = np.random.default_rng(m + n)
     xq = rng.integers(-127, 128, (m, k), dtype=np.int8)
     wq = rng.integers(-127, 128, (k, n), dtype=np.int8)
     a = (rng.random(m, dtype=np.float32) * 0.05 + 1e-3).astype(np.float32)
@@ -249,6 +270,8 @@ def _fused_case(device, batch, length, heads, k, scale_dtype, gain, seed):
     (1, 40, 3, 128, torch.bfloat16, 0.3),
     (7, 3, 2, 128, torch.bfloat16, 0.5),                # sequences shorter than a read-back step
     (5, 67, 2, 128, torch.bfloat16, 128 ** -0.5),       # batch entries wrapping inside every tile
+    (2, 2176, 24, 128, torch.float32, 128 ** -0.5),     # rounds order, batch entries wrapping in 192-token tiles
+    (3, 1300, 24, 128, torch.bfloat16, 0.5),            # rounds order, ragged last token tile
 ])
 def test_fused_projection_qk_prep_bit_exact(device, batch, length, heads, k, scale_dtype, gain):
     """flk_w8a8_qk_prep == flk_qk_prep(flk_w8a8_gemm(...)) bit for bit: the epilogue applies
