@@ -449,15 +449,14 @@ struct GemmProblem {
 struct GemmGroup {
   GemmProblem p[2];
   int first_blocks;
-  int rounds;   // one problem, rounds order (w8a8_gemm_kernel)
+  int units;    // tiles of both problems (first_blocks + p[1]'s, or first_blocks alone)
+  int rounds;   // rounds order (w8a8_gemm_kernel)
 };
 
-// kAcc: also write the exact int32 products (a test and debugging path).
-// kQk: instead of Y, run qk_prep on each finished bf16 head row (kScaleF32: float32 norm
-// scales) and write head-major q, k, v.
 // One output tile: channels n0 .. n0 + 255 and tokens m0 .. m0 + 64 kMF - 1 (kMF = 4: 256
 // tokens; 3: 192), of which tokens below m_limit are stored.  Each of the 2 (channels) x 4
-// (tokens) waves holds 128 channels x 16 kMF tokens.
+// (tokens) waves holds 128 channels x 16 kMF tokens.  kAcc, kQk, kScaleF32 as for
+// w8a8_gemm_kernel.
 template <bool kAcc, bool kQk, bool kScaleF32, int kMF>
 __device__ __forceinline__ void gemm_tile(uint8_t* smem, const GemmProblem& P, int m0, int n0, int m_limit) {
   constexpr int kWaveM = 16 * kMF;   // a wave's tokens
@@ -710,21 +709,25 @@ __device__ __forceinline__ void tile_of(int u, int tiles_m, int tiles_n, int& mt
   nt = in_group / gm;
 }
 
-// The rounds order's 192-token tiles: logical tiles [first, end) taken as runs of one channel
-// tile (consecutive token tiles of one group), each run's tokens cut into 192-token tiles, the
-// last one short.  The j-th such tile, or false past the last.  The host's
-// gemm_rounds_grid counts them the same way.
-__device__ __forceinline__ bool leftover_tile(int first, int end, int tiles_m, int tiles_n, int M, int j, int& m0,
+// The rounds order's 192-token tiles: logical tiles [first, end) of a launch's problems (p[0]'s
+// tiles, then p[1]'s) taken as runs of one channel tile (consecutive token tiles of one group
+// of one problem), each run's tokens cut into 192-token tiles, the last one short.  The j-th
+// such tile, or false past the last.  The host's gemm_rounds_grid counts them the same way.
+__device__ __forceinline__ bool leftover_tile(const GemmGroup& grp, int first, int end, int j, int& second, int& m0,
                                               int& n0, int& m_end) {
   for (int u = first; u < end;) {
-    const int group_tiles = kGroup * tiles_n;
-    const int group = u / group_tiles;
+    second = u >= grp.first_blocks;
+    const GemmProblem& P = second ? grp.p[1] : grp.p[0];
+    const int base = second ? grp.first_blocks : 0;
+    const int p_end = second ? end : min(end, grp.first_blocks);
+    const int group_tiles = kGroup * P.tiles_n;
+    const int group = (u - base) / group_tiles;
     const int first_m = group * kGroup;
-    const int gm = min(kGroup, tiles_m - first_m);
-    const int in_group = u - group * group_tiles;
+    const int gm = min(kGroup, P.tiles_m - first_m);
+    const int in_group = u - base - group * group_tiles;
     const int r = in_group % gm;
-    const int run = min(gm - r, end - u);
-    const int s = (first_m + r) * kGT, e = min((first_m + r + run) * kGT, M);
+    const int run = min(gm - r, p_end - u);
+    const int s = (first_m + r) * kGT, e = min((first_m + r + run) * kGT, P.M);
     const int count = (e - s + kGT192 - 1) / kGT192;
     if (j < count) {
       m0 = s + j * kGT192;
@@ -746,24 +749,26 @@ __global__ __launch_bounds__(kGThreads, 2) void w8a8_gemm_kernel(const GemmGroup
   __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * kGStage];
   const int xcd = blockIdx.x % kXcds, local = blockIdx.x / kXcds;   // blocks are dealt round-robin over XCDs
   if (grp.rounds) {
-    // Rounds order (one problem): each XCD takes a contiguous range of the logical tiles, runs
-    // whole rounds of 32 of them, and cuts the ones left over into 192-token tiles, so the
-    // partial last round has up to 4/3 as many blocks with 3/4 of the work each.
+    // Rounds order: each XCD takes a contiguous range of the logical tiles (of one problem,
+    // then the next), runs whole rounds of 32 of them, and cuts the ones left over into
+    // 192-token tiles, so the partial last round has up to 4/3 as many blocks with 3/4 of the
+    // work each.
     constexpr int C = kCUs / kXcds;
-    const GemmProblem& P = grp.p[0];
-    const int units = P.tiles_m * P.tiles_n;
-    const int ux0 = (int)((int64_t)xcd * units / kXcds);
-    const int n = (int)((int64_t)(xcd + 1) * units / kXcds) - ux0;
+    const int ux0 = (int)((int64_t)xcd * grp.units / kXcds);
+    const int n = (int)((int64_t)(xcd + 1) * grp.units / kXcds) - ux0;
     const int full = n / C * C;
     if (local < full) {
+      const int u = ux0 + local;
+      const bool second = u >= grp.first_blocks;
+      const GemmProblem& P = second ? grp.p[1] : grp.p[0];
       int mt, nt;
-      tile_of(ux0 + local, P.tiles_m, P.tiles_n, mt, nt);
+      tile_of(u - (second ? grp.first_blocks : 0), P.tiles_m, P.tiles_n, mt, nt);
       gemm_tile<kAcc, kQk, kScaleF32, 4>(smem, P, mt * kGT, nt * kGT, P.M);
       return;
     }
-    int m0, n0, m_end;
-    if (!leftover_tile(ux0 + full, ux0 + n, P.tiles_m, P.tiles_n, P.M, local - full, m0, n0, m_end)) return;
-    gemm_tile<kAcc, kQk, kScaleF32, 3>(smem, P, m0, n0, m_end);
+    int second, m0, n0, m_end;
+    if (!leftover_tile(grp, ux0 + full, ux0 + n, local - full, second, m0, n0, m_end)) return;
+    gemm_tile<kAcc, kQk, kScaleF32, 3>(smem, second ? grp.p[1] : grp.p[0], m0, n0, m_end);
     return;
   }
   // Tile order: renumber so that each XCD runs a contiguous range of logical tiles (of one
@@ -943,24 +948,28 @@ namespace {
 
 int64_t problem_blocks(const GemmProblem& p) { return (int64_t)p.tiles_m * p.tiles_n; }
 
-// Grid of the rounds order of one problem (w8a8_gemm_kernel), or 0 when it is not the choice:
-// it needs a full round of 32 tiles on every XCD, tiles left over, and at most one round of
+// Grid of the rounds order of a launch (w8a8_gemm_kernel), or 0 when it is not the choice: it
+// needs a full round of 32 tiles on every XCD, tiles left over, and at most one round of
 // 192-token tiles for them (counted as leftover_tile walks them).
-int64_t gemm_rounds_grid(const GemmProblem& p) {
+int64_t gemm_rounds_grid(const GemmGroup& g) {
   constexpr int C = kCUs / kXcds;
-  const int64_t units = problem_blocks(p);
-  if (units < kCUs || units > INT32_MAX) return 0;
+  const int64_t units = g.units;
+  if (units < kCUs) return 0;
   int64_t most = 0, left_max = 0;
   for (int x = 0; x < kXcds; ++x) {
     const int64_t ux0 = x * units / kXcds, n = (x + 1) * units / kXcds - ux0;
     const int64_t full = n / C * C;
     int64_t count = 0;
     for (int64_t u = ux0 + full; u < ux0 + n;) {
+      const bool second = u >= g.first_blocks;
+      const GemmProblem& p = second ? g.p[1] : g.p[0];
+      const int64_t base = second ? g.first_blocks : 0;
+      const int64_t p_end = second ? ux0 + n : std::min<int64_t>(ux0 + n, g.first_blocks);
       const int64_t group_tiles = (int64_t)kGroup * p.tiles_n;
-      const int64_t group = u / group_tiles, first_m = group * kGroup;
+      const int64_t group = (u - base) / group_tiles, first_m = group * kGroup;
       const int64_t gm = std::min<int64_t>(kGroup, p.tiles_m - first_m);
-      const int64_t r = (u - group * group_tiles) % gm;
-      const int64_t run = std::min(gm - r, ux0 + n - u);
+      const int64_t r = (u - base - group * group_tiles) % gm;
+      const int64_t run = std::min(gm - r, p_end - u);
       const int64_t e = std::min<int64_t>((first_m + r + run) * kGT, p.M);
       count += (e - (first_m + r) * kGT + kGT192 - 1) / kGT192;
       u += run;
@@ -970,6 +979,14 @@ int64_t gemm_rounds_grid(const GemmProblem& p) {
     most = std::max(most, full + count);
   }
   return left_max > 0 ? most * kXcds : 0;
+}
+
+// Fills a launch's tile count and order; returns its grid.
+int64_t plan_group(GemmGroup& g, int64_t units) {
+  g.units = (int)std::min<int64_t>(units, INT32_MAX);
+  const int64_t rounds = units <= INT32_MAX ? gemm_rounds_grid(g) : 0;
+  g.rounds = rounds > 0;
+  return rounds ? rounds : units;
 }
 
 template <bool kAcc, bool kQk, bool kScaleF32>
@@ -1053,10 +1070,8 @@ extern "C" int flk_w8a8_gemm(const int8_t* xq, const int8_t* wq_t, const float* 
   p.tiles_m = (m + kGT - 1) / kGT;
   p.tiles_n = (n + kGT - 1) / kGT;
   g.p[1] = p;
-  const int64_t rounds = gemm_rounds_grid(p);
-  const int64_t blocks = rounds ? rounds : problem_blocks(p);
   g.first_blocks = (int)std::min<int64_t>(problem_blocks(p), INT32_MAX);
-  g.rounds = rounds > 0;
+  const int64_t blocks = plan_group(g, problem_blocks(p));
   return acc_or_null ? launch_group<true, false, false>(g, blocks, stream)
                      : launch_group<false, false, false>(g, blocks, stream);
 }
@@ -1071,10 +1086,8 @@ extern "C" int flk_w8a8_qk_prep(const int8_t* xq, const int8_t* wq_t, const floa
                             batch, length, num_heads, head_dim, q_out, k_out, v_out, out_length, out_offset, g.p[0]);
   if (st != FLK_OK) return st == kNoWork ? FLK_OK : st;
   g.p[1] = g.p[0];
-  const int64_t rounds = gemm_rounds_grid(g.p[0]);
-  const int64_t blocks = rounds ? rounds : problem_blocks(g.p[0]);
   g.first_blocks = (int)std::min<int64_t>(problem_blocks(g.p[0]), INT32_MAX);
-  g.rounds = rounds > 0;
+  const int64_t blocks = plan_group(g, problem_blocks(g.p[0]));
   return launch_qk(g, blocks, scale_is_f32, stream);
 }
 
@@ -1100,7 +1113,7 @@ extern "C" int flk_w8a8_qk_prep_pair(
   if (st1 == kNoWork) g.p[1] = g.p[0];
   const bool both = st0 == FLK_OK && st1 == FLK_OK;
   const int64_t b0 = problem_blocks(g.p[0]);
-  const int64_t blocks = both ? b0 + problem_blocks(g.p[1]) : b0;
   g.first_blocks = (int)std::min<int64_t>(b0, INT32_MAX);
+  const int64_t blocks = plan_group(g, both ? b0 + problem_blocks(g.p[1]) : b0);
   return launch_qk(g, blocks, scale_is_f32, stream);
 }
