@@ -37,11 +37,11 @@
 // share an XCD (and its L2), and grouped so that 4 token tiles sweep the channel tiles
 // together.
 //
-// A one-problem launch of more than one round (the Klein projection: 648 tiles, 2.53 rounds
-// of 256 CUs) takes the rounds order: each XCD runs whole rounds of 32 of its tiles, then
-// cuts the tiles left over into tiles of 192 tokens (waves of 128 x 48: three token
-// fragments), so the partial last round has up to 4/3 as many blocks with 3/4 of the work
-// each (measured 1-5% faster for the plain GEMM, 3-6% with the qk_prep epilogue).
+// A launch of more than one round (the Klein projection: 648 tiles, 2.53 rounds of 256 CUs)
+// takes the rounds order: each XCD runs whole rounds of 32 of its tiles, then cuts the tiles
+// left over into tiles of 192 tokens (waves of 128 x 48: three token fragments), so the
+// partial last round has up to 4/3 as many blocks with 3/4 of the work each (measured 1-5%
+// faster for the plain GEMM, 3-6% with the qk_prep epilogue).
 //
 // A launch takes up to two problems (GemmGroup; the activation quantiser likewise takes a
 // QuantGroup): a double block's text and image projections share one grid, so the small
