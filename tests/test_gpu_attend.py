@@ -99,6 +99,31 @@ def test_attend_rounds_launch_equals_one_head_at_a_time(device, batch, heads, le
                    P.attend_bounded(*(to_np(t[sl]) for t in (q, k, v))))
 
 
+def test_attend_random_shapes_every_launch_equals_one_head_at_a_time(device):
+    """Seeded random shapes, each launched whole (flk_attend picks 256-query tiles, 192-query
+    tiles or the rounds launch; the name it reports is checked against the three) and one head
+    at a time: every head is the same bit for bit, whatever tiling the whole grid took."""
+    rng = np.random.default_rng(2024)
+    seen = set()
+    for trial in range(8):
+        while True:   # alternately more and fewer than 256 tiles of 256 queries
+            batch, heads, length = int(rng.integers(1, 4)), int(rng.integers(1, 41)), int(rng.integers(1, 5200))
+            tiles = batch * heads * -(-length // 256)
+            if (256 < tiles <= 700) if trial % 2 == 0 else (tiles <= 256):
+                break
+        name = _lib.attend_kernel_name(batch, heads, length)
+        assert name in ("attend_kernel", "attend_tile192_kernel", "attend_rounds_kernel"), name
+        seen.add(name)
+        q, k, v = prepped_case(batch, heads, length, seed=100 + trial)
+        got = run_attend(q, k, v, device, splits=1)
+        for b in range(batch):
+            for h in range(heads):
+                one = run_attend(*(t[b:b + 1, h:h + 1] for t in (q, k, v)), device, splits=1)
+                assert np.array_equal(got[b:b + 1, h:h + 1].view(np.uint32), one.view(np.uint32)), \
+                    (batch, heads, length, name, b, h)
+    print("launches exercised:", sorted(seen))
+
+
 def test_attend_peaked_logits(device):
     """Large norm scales (bound 11.3 * 2.4^2 = 65 < 80): far-from-uniform attention."""
     q, k, v = prepped_case(1, 2, 512, seed=5, scale=2.4)
