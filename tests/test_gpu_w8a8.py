@@ -186,6 +186,30 @@ def test_gemm_rounds_order_bit_exact(device, m, n):
     assert_bits_equal(y, Q.rescale(acc_want, a, ws), f"y {m}x{k}x{n}")
 
 
+def test_gemm_random_shapes_bit_exact(device):
+    """Seeded random projections around one round of tiles (some take the rounds order, some
+    the plain order, ragged edges in both dimensions): every int32 product and bf16 output
+    against the oracle."""
+    rng = np.random.default_rng(77)
+    for trial in range(6):
+        while True:
+            m, n = int(rng.integers(1, 9000)), 4 * int(rng.integers(1, 3000))
+            if 200 <= -(-m // 256) * -(-n // 256) <= 700:
+                break
+        k = 128 * int(rng.integers(1, 3))
+        xq = rng.integers(-127, 128, (m, k), dtype=np.int8)
+        wq = rng.integers(-127, 128, (k, n), dtype=np.int8)
+        a = (rng.random(m, dtype=np.float32) * 0.05 + 1e-3).astype(np.float32)
+        ws = (rng.random(n, dtype=np.float32) * 0.002 + 1e-5).astype(np.float32)
+        acc = torch.empty((m, n), dtype=torch.int32, device=device)
+        y = w8a8.gemm(torch.from_numpy(xq).to(device), torch.from_numpy(a).to(device),
+                      torch.from_numpy(np.ascontiguousarray(wq.T)).to(device), torch.from_numpy(ws).to(device),
+                      acc=acc)
+        acc_want = Q.int_gemm(xq, wq)
+        np.testing.assert_array_equal(host(acc), acc_want, err_msg=f"{m}x{k}x{n}")
+        assert_bits_equal(y, Q.rescale(acc_want, a, ws), f"y {m}x{k}x{n}")
+
+
 def test_gemm_extreme_operands(device):
     """All operands at +-127: the largest |acc| the int32 accumulator sees at K = 3072."""
     m, k, n = 64, 3072, 64
