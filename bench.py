@@ -9,14 +9,16 @@ launch stream (torch's current stream) -> ms_per_step.  Before it run `--warmup`
 steps and then untimed steps for `--clock-warmup-s` seconds (reported as clock_warmup_s):
 the GPU takes about a second of load to reach its working clock, which a few warm-up steps
 do not give.  Each kernel is then timed alone the same way, `--kernel-launches`
-back-to-back launches over the same rotating buffers, which gives its average launch
+back-to-back launches over the same rotating buffers after `--leg-warmup-s` seconds of
+untimed ones (the clock falls while the host sets a leg up), which gives its average launch
 duration: `value` is attend's TFLOP/s from that, and the line also reports
 qk_prep's GB/s and both roofline fractions.  To keep the QKV input from being
 served by the 256 MB Infinity Cache between steps, steps rotate over buffer sets
 whose total exceeds it.  A CPU baseline (the torch-CPU restatement of the reference's
 plain-XLA path, the oracle) is timed on the host cores.  `head_share` times attend on one
 GPU's share of an 8-way head-parallel run (3 of the 24 heads, the full sequence), the grid
-that the key-split path exists for.
+that the key-split path exists for.  `vendor` times the same operations through ROCm's own
+libraries (torch's flash SDPA, hipBLASLt's int8 and bf16 GEMMs) for comparison.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload klein_1024]
 
@@ -62,6 +64,8 @@ def parse():
                     help="further untimed steps, for this many seconds, before the timed region: the "
                          "GPU needs ~1 s of load to settle at its working clock whatever --warmup is; "
                          "reported as clock_warmup_s (0 = off)")
+    ap.add_argument("--leg-warmup-s", type=float, default=0.5,
+                    help="back-to-back untimed calls, for this many seconds, before each per-kernel leg")
     ap.add_argument("--kernel-launches", type=int, default=200,
                     help="back-to-back launches of each kernel alone behind its average launch duration")
     ap.add_argument("--workload", default="klein_1024")
@@ -69,6 +73,8 @@ def parse():
                     help="time each kernel leg as eager back-to-back launches instead of a replayed HIP graph")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-w8a8", action="store_true", help="skip the int8 W8A8 QKV projection leg")
+    ap.add_argument("--no-vendor", action="store_true",
+                    help="skip the comparison legs through ROCm's libraries (torch SDPA flash, hipBLASLt GEMMs)")
     ap.add_argument("--projection", default="qkv_1024")
     ap.add_argument("--cpu-reps", type=int, default=9,
                     help="timed CPU-baseline steps (after 3 warm-up steps); the p50 is reported")
@@ -252,6 +258,52 @@ def head_share_leg(w, qkv_heads, timed) -> dict:
     return {"heads": heads, "of_gpus": SHARE_GPUS, "splits": splits, "avg_launch_us": round(split_ms * 1e3, 2),
             "achieved": round(flops / (split_ms * 1e-3) / 1e12, 1), "unit": "TFLOP/s",
             "unsplit_us": round(plain_ms * 1e3, 2)}
+
+
+def vendor_leg(w, qkv_sets, attend_us, gemm_us, args, timed, dev) -> dict:
+    """The same operations through ROCm's own libraries, for comparison: torch's fused SDPA
+    (the flash backend only, no fallback to the unfused math path) on the same rotating
+    head-major q, k, v as attend, with scale 1 as attend applies (q carries the 1/sqrt(d)
+    gain); hipBLASLt's int8 GEMM (torch._int_mm, int32 output, no rescale) and its bf16
+    GEMM (the unquantised projection, what the reference's nn.Linear runs) on the
+    projection's operands.  Eager back-to-back launches."""
+    import torch
+    import torch.nn.functional as F
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    from flicker_amd import workloads
+
+    out = {}
+    n = min(args.kernel_launches, 50)
+    try:
+        with sdpa_kernel([SDPBackend.FLASH_ATTENTION]):
+            for i in range(10):
+                F.scaled_dot_product_attention(*qkv_sets[i % len(qkv_sets)], scale=1.0)
+            ms = timed(lambda i: F.scaled_dot_product_attention(*qkv_sets[i % len(qkv_sets)], scale=1.0), n)
+        tflops = w.attend_flops() / (ms * 1e-3) / 1e12
+        out["sdpa_flash"] = {"avg_launch_us": round(ms * 1e3, 2), "achieved": round(tflops, 1),
+                             "unit": "TFLOP/s", "attend_speedup": round(ms * 1e3 / attend_us, 3),
+                             "fa_library": str(torch.backends.cuda.preferred_rocm_fa_library())}
+    except RuntimeError as e:   # no flash kernel for this build or shape
+        out["sdpa_flash"] = {"error": str(e)[:200]}
+    if args.no_w8a8:
+        return out
+    p = workloads.PROJECTIONS[args.projection]
+    x, qw, xq, _ = projection_operands(p, dev)
+    b = qw.wq_t.t()   # (K, N), column-major: hipBLASLt's preferred int8 layout
+    for _ in range(10):
+        torch._int_mm(xq, b)
+    ms = timed(lambda i: torch._int_mm(xq, b), n)
+    out["int_mm"] = {"avg_launch_us": round(ms * 1e3, 2), "achieved": round(p.gemm_ops() / (ms * 1e-3) / 1e12, 1),
+                     "unit": "TOP/s", "output": "int32", "w8a8_gemm_speedup": round(ms * 1e3 / gemm_us, 3)}
+    wb = workloads.make_projection(p)[1].t().contiguous().to(dev)   # nn.Linear's (out, in) weight
+    for _ in range(10):
+        F.linear(x, wb)
+    ms = timed(lambda i: F.linear(x, wb), n)
+    out["bf16_linear"] = {"avg_launch_us": round(ms * 1e3, 2),
+                          "achieved": round(p.gemm_ops() / (ms * 1e-3) / 1e12, 1), "unit": "TFLOP/s",
+                          "w8a8_gemm_speedup": round(ms * 1e3 / gemm_us, 3)}
+    return out
 
 
 def w8a8_leg(args, timed, dev) -> dict:
@@ -479,6 +531,10 @@ def main() -> int:
                 fn(i)
         graph.replay()
         torch.cuda.synchronize()
+        t0 = time.perf_counter()   # the GPU idled during the capture: replays until its clock is back
+        while time.perf_counter() - t0 < args.leg_warmup_s:
+            graph.replay()
+            torch.cuda.synchronize()
         reps = max(1, -(-n // calls))
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
@@ -518,7 +574,21 @@ def main() -> int:
             legs[name] = {"eager_us": round(eager * 1e3, 2), "graph_us": round(graph * 1e3, 2)}
         return min(eager, graph)
 
-    kernel_timed = timed if args.eager_kernel_timing else timed_min
+    def settled(timing):
+        """`timing` preceded by back-to-back calls for --leg-warmup-s seconds: a leg often
+        follows host-side setup during which the GPU idled and its clock fell, and the clock
+        takes a fraction of a second of load to recover."""
+        def run(fn, n, name=None):
+            t0, i = time.perf_counter(), 0
+            while time.perf_counter() - t0 < args.leg_warmup_s:
+                for _ in range(10):
+                    fn(i)
+                    i += 1
+                torch.cuda.synchronize()
+            return timing(fn, n, name) if name else timing(fn, n)
+        return run
+
+    kernel_timed = settled(timed if args.eager_kernel_timing else timed_min)
     qk_ms = kernel_timed(run_qk, n_kernel, "qk_prep") if args.only == "step" else step_ms
     at_ms = kernel_timed(run_attend, n_kernel, "attend") if args.only == "step" else step_ms
     qk_gbs = w.qk_prep_bytes() / (qk_ms * 1e-3) / 1e9
@@ -569,6 +639,7 @@ def main() -> int:
         "clock_warmup_s": round(clock_warmup_s, 2),
         "clock_warmup_steps": clock_steps,
         "kernel_launches": n_kernel if args.only == "step" else None,
+        "leg_warmup_s": args.leg_warmup_s,
         "kernel_timing": "eager back-to-back launches" if args.eager_kernel_timing else
                          "min of eager back-to-back launches and a replayed HIP graph",
         "kernel_timings": legs or None,
@@ -612,6 +683,9 @@ def main() -> int:
         if "w8a8_gemm" in traffic and proj.tokens == w.batch * w.length:
             result["w8a8"]["roofline"]["traffic"] = round(traffic["w8a8_gemm"]["traffic_bytes"])
             result["w8a8"]["roofline"]["traffic_source"] = source
+    if not args.no_vendor and args.only == "step":
+        gemm_us = result["w8a8"]["roofline"]["avg_launch_us"] if "w8a8" in result else None
+        result["vendor"] = vendor_leg(w, [s[1] for s in sets], at_ms * 1e3, gemm_us, args, settled(timed), dev)
     if not args.no_cpu_baseline and args.only == "step":
         result["cpu_baseline"] = cpu_baseline(w, qkv_cpu, qs_cpu, ks_cpu, ids, args.cpu_reps)
     print(json.dumps(result), flush=True)
