@@ -884,12 +884,14 @@ int check_attend(const void* q, const void* k, const void* v, void* o, int batch
       !flk_host_aligned(o, 8) || o_batch_stride % 4 || o_head_stride % 4 || o_row_stride % 4)
     return FLK_E_ALIGN;
   if (o_batch_stride < 0 || o_head_stride < 0 || o_row_stride < kD) return FLK_E_INVALID;
-  if ((int64_t)((length + kBM - 1) / kBM) * batch * heads > INT32_MAX) return FLK_E_INVALID;
+  // Query and key positions up to a tile past the end stay within int in the kernels.
+  if (length > INT32_MAX - kBM) return FLK_E_INVALID;
+  if (((int64_t)length + kBM - 1) / kBM * batch * heads > INT32_MAX) return FLK_E_INVALID;
   return FLK_OK;
 }
 
-int64_t q_tiles(int length) { return (length + kBM - 1) / kBM; }
-int key_groups(int length) { return ((length + kBN - 1) / kBN + 3) / 4; }
+int64_t q_tiles(int length) { return ((int64_t)length + kBM - 1) / kBM; }
+int key_groups(int length) { return (int)((((int64_t)length + kBN - 1) / kBN + 3) / 4); }
 
 // Workspace of a split launch: per split and (b, h, 256-query tile), 512 lanes x (64 acc + 1 l)
 // floats.
@@ -899,7 +901,7 @@ int64_t split_workspace_bytes(int batch, int heads, int length, int splits) {
 
 // 192-query tiles when the grid fits the CUs in one round with them as with 256-query tiles:
 // the launch then takes the time of one block, and a 192-query block does 3/4 of the work.
-int64_t q_tiles192(int length) { return (length + kBM192 - 1) / kBM192; }
+int64_t q_tiles192(int length) { return ((int64_t)length + kBM192 - 1) / kBM192; }
 
 bool tile192_preferred(int batch, int heads, int length) {
   const int64_t bh = (int64_t)batch * heads;
@@ -1008,9 +1010,10 @@ int64_t balanced_workspace_bytes(int grid) { return balanced_counters_offset(gri
 bool balanced_preferred(int batch, int heads, int length) {
   const int64_t units = q_tiles(length) * batch * heads;
   constexpr int C = kCUs / kXcds;
-  if (units < kCUs || units > INT32_MAX || (int64_t)(length + kBN - 1) / kBN * 1024 > INT32_MAX) return false;
+  const int64_t key_tiles = ((int64_t)length + kBN - 1) / kBN;
+  if (units < kCUs || units > INT32_MAX || key_tiles * 1024 > INT32_MAX) return false;
   const int64_t left = ((units + kXcds - 1) / kXcds) % C;   // leftover tiles of the fullest XCD
-  return left > 0 && left <= 16 && left * ((length + kBN - 1) / kBN) >= 16 * C;
+  return left > 0 && left <= 16 && left * key_tiles >= 16 * C;
 }
 
 }  // namespace
@@ -1032,7 +1035,7 @@ extern "C" int flk_attend_balanced_to(const void* q, const void* k, const void* 
                               o_row_stride);
   if (st != FLK_OK) return st == kNothing ? FLK_OK : st;
   const int64_t units = q_tiles(length) * batch * heads;   // <= INT32_MAX (check_attend)
-  if ((int64_t)(length + kBN - 1) / kBN * 1024 > INT32_MAX) return FLK_E_UNSUPPORTED;   // 32-bit split math
+  if (((int64_t)length + kBN - 1) / kBN * 1024 > INT32_MAX) return FLK_E_UNSUPPORTED;   // 32-bit split math
   constexpr int grid = kCUs;
   if (!workspace || workspace_bytes < balanced_workspace_bytes(grid)) return FLK_E_INVALID;
   if (!flk_host_aligned(workspace, 16)) return FLK_E_ALIGN;

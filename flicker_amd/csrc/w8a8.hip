@@ -390,6 +390,7 @@ constexpr int kGNF = kGWaveN / 16;       // channel fragments per wave
 constexpr int kGCopies = kGT / kGWaves / 8;   // WqT copy instructions per wave and stage (4)
 constexpr int kGT192 = 192;              // token edge of the tiles that re-tile a partial last round
 constexpr int kGRing = 4;                // channel-fragment registers in flight
+constexpr int kMaxDim = INT32_MAX - kGT;  // largest token / channel count: a tile past it stays within int
 constexpr int kGLead = 3;                // groups between a channel fragment's read and its MFMAs
 static_assert(kGNF % kGRing == 0 && kGRing > kGLead, "the fragment ring must divide the groups of a step");
 #ifndef FLK_GEMM_GROUP
@@ -1014,7 +1015,7 @@ int qk_problem(const int8_t* xq, const int8_t* wq_t, const float* a_scale, const
   if (k % 128) return FLK_E_UNSUPPORTED;
   if ((int64_t)k * 127 * 127 > INT32_MAX) return FLK_E_UNSUPPORTED;
   const int64_t m64 = (int64_t)batch * length, n = 3LL * num_heads * head_dim;
-  if (m64 > INT32_MAX || n > INT32_MAX) return FLK_E_INVALID;
+  if (m64 > kMaxDim || n > kMaxDim) return FLK_E_INVALID;
   if (!flk_host_aligned(xq, 16) || !flk_host_aligned(wq_t, 16) || !flk_host_aligned(w_scale, 16) ||
       !flk_host_aligned(a_scale, 4) || !flk_host_aligned(cos, 16) || !flk_host_aligned(sin, 16) ||
       table_row_stride % 4 || !flk_host_aligned(q_scale, 16) || !flk_host_aligned(k_scale, 16) ||
@@ -1048,6 +1049,7 @@ extern "C" int flk_w8a8_gemm(const int8_t* xq, const int8_t* wq_t, const float* 
                              void* stream) {
   if (m < 0 || k < 0 || n < 0 || y_row_stride < n) return FLK_E_INVALID;
   if (m == 0 || n == 0) return FLK_OK;
+  if (m > kMaxDim || n > kMaxDim) return FLK_E_INVALID;
   if (!xq || !wq_t || !a_scale || !w_scale || !y || k == 0) return FLK_E_INVALID;
   if (k % 128 || n % 4) return FLK_E_UNSUPPORTED;
   if ((int64_t)k * 127 * 127 > INT32_MAX) return FLK_E_UNSUPPORTED;   // int32 accumulation must be exact

@@ -68,6 +68,9 @@ def test_attend_validation(lib):
     assert f(FAKE + 8, FAKE, FAKE, FAKE, 1, 24, 4608, 128, None) == _lib.FLK_E_ALIGN
     assert f(None, FAKE, FAKE, FAKE, 1, 24, 4608, 128, None) == _lib.FLK_E_INVALID
     assert f(FAKE, FAKE, FAKE, FAKE, 0, 24, 4608, 128, None) == _lib.FLK_OK       # empty: nothing launched
+    # positions up to a tile past the end must stay within int
+    assert f(FAKE, FAKE, FAKE, FAKE, 1, 1, 2 ** 31 - 1, 128, None) == _lib.FLK_E_INVALID
+    assert f(FAKE, FAKE, FAKE, FAKE, 1, 1, 2 ** 31 - 256, 128, None) == _lib.FLK_E_INVALID
     g = lib.flk_attend_to
     hd = 24 * 128
     assert g(FAKE, FAKE, FAKE, FAKE, 1, 24, 4608, 128, 4608 * hd, 128, hd + 2, None) == _lib.FLK_E_ALIGN
@@ -356,6 +359,9 @@ def test_w8a8_validation(lib):
     assert lib.flk_w8a8_gemm(FAKE, FAKE, FAKE, FAKE, 64, 256, 64, FAKE, 32, None, None) == _lib.FLK_E_INVALID
     assert lib.flk_w8a8_gemm(FAKE, FAKE, FAKE, FAKE, 64, 256, 64, FAKE + 4, 64, None, None) == _lib.FLK_E_ALIGN
     assert lib.flk_w8a8_gemm(FAKE, FAKE, FAKE, FAKE, 64, 2 ** 20, 64, FAKE, 64, None, None) == _lib.FLK_E_UNSUPPORTED
+    big = 2 ** 31 - 1   # token / channel counts whose last tile would pass the int range
+    assert lib.flk_w8a8_gemm(FAKE, FAKE, FAKE, FAKE, big, 256, 64, FAKE, 64, None, None) == _lib.FLK_E_INVALID
+    assert lib.flk_w8a8_gemm(FAKE, FAKE, FAKE, FAKE, 64, 256, big - 3, FAKE, big - 3, None, None) == _lib.FLK_E_INVALID
     assert lib.flk_w8a8_gemm(FAKE, FAKE, FAKE, FAKE, 0, 256, 64, FAKE, 64, None, None) == _lib.FLK_OK
     assert lib.flk_quantize_act(FAKE, 3000, FAKE, 8, 3072, FAKE, FAKE, None) == _lib.FLK_E_INVALID
     assert lib.flk_quantize_act(FAKE, 3076, FAKE, 8, 3076, FAKE, FAKE, None) == _lib.FLK_E_UNSUPPORTED
