@@ -269,6 +269,7 @@ int check_common(const void* qkv, int64_t qkv_batch_stride, int64_t qkv_row_stri
       out_offset + length > out_length)
     return FLK_E_INVALID;
   if (batch == 0 || length == 0) return kEmpty;
+  if (length > INT32_MAX - kTokensPerBlock) return FLK_E_INVALID;   // token index of the last block's lanes
   if (qkv_row_stride < 3LL * num_heads * head_dim ||
       (batch > 1 && qkv_batch_stride < (int64_t)(length - 1) * qkv_row_stride + 3LL * num_heads * head_dim))
     return FLK_E_INVALID;
@@ -282,7 +283,7 @@ int check_common(const void* qkv, int64_t qkv_batch_stride, int64_t qkv_row_stri
 
 template <bool kIds>
 int dispatch(int hpg, int batch, int scale_is_f32, hipStream_t stream, const Launch& a) {
-  const dim3 grid((a.length + kTokensPerBlock - 1) / kTokensPerBlock, a.num_heads / hpg, batch);
+  const dim3 grid((unsigned)(((int64_t)a.length + kTokensPerBlock - 1) / kTokensPerBlock), a.num_heads / hpg, batch);
   const bool gain = a.q_gain != 1.0f;
   if (scale_is_f32) {
     if (gain) launch<true, true, kIds>(hpg, grid, stream, a);

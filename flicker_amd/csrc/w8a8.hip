@@ -831,6 +831,7 @@ extern "C" int flk_quantize_weight(const void* w, int64_t w_row_stride, const fl
                                    int8_t* wq_t, float* w_scale, void* stream) {
   if (k < 0 || n < 0 || w_row_stride < n) return FLK_E_INVALID;
   if (k == 0 || n == 0) return FLK_OK;
+  if (k > INT32_MAX - 64 || n > INT32_MAX - 64) return FLK_E_INVALID;   // a block's last row / column index
   if (!w || !s || !wq_t || !w_scale) return FLK_E_INVALID;
   if (k % 64 || n % 8 || w_row_stride % 8) return FLK_E_UNSUPPORTED;
   if (!flk_host_aligned(w, 16) || !flk_host_aligned(wq_t, 16) || !flk_host_aligned(s, 4) ||
@@ -872,7 +873,7 @@ int modulated_problem(const void* x, int64_t x_row_stride, const void* shift, co
   if (m < 0 || k < 0 || x_row_stride < k || mod_batch_stride < 0 || (x_mod && x_mod_row_stride < k))
     return FLK_E_INVALID;
   if (m == 0 || k == 0) return kNoWork;   // an empty input (its sequence length may be 0 too)
-  if (tokens_per_batch <= 0) return FLK_E_INVALID;
+  if (tokens_per_batch <= 0 || m > INT32_MAX - 4) return FLK_E_INVALID;
   if (!x || !shift || !scale || !inv_s || !xq || !a_scale) return FLK_E_INVALID;
   if ((m - 1) / tokens_per_batch > 0 && mod_batch_stride < k) return FLK_E_INVALID;
   if (k % 8 || k > 8192) return FLK_E_UNSUPPORTED;
@@ -894,6 +895,7 @@ extern "C" int flk_quantize_act(const void* x, int64_t x_row_stride, const float
                                 int8_t* xq, float* a_scale, void* stream) {
   if (m < 0 || k < 0 || x_row_stride < k) return FLK_E_INVALID;
   if (m == 0 || k == 0) return FLK_OK;
+  if (m > INT32_MAX - 4) return FLK_E_INVALID;   // the last block's row index
   if (!x || !inv_s || !xq || !a_scale) return FLK_E_INVALID;
   if (k % 8 || k > 8192) return FLK_E_UNSUPPORTED;
   if (x_row_stride % 8 || !flk_host_aligned(x, 16) || !flk_host_aligned(inv_s, 16) || !flk_host_aligned(xq, 8) ||

@@ -181,6 +181,7 @@ def test_qk_prep_validation(lib):
 
     assert call(d=64) == _lib.FLK_E_UNSUPPORTED
     assert call(oo=1) == _lib.FLK_E_INVALID                 # out_offset + L > out_length
+    assert call(l=2 ** 31 - 1, ol=2 ** 31 - 1) == _lib.FLK_E_INVALID   # last block's token index past int
     assert call(rs=9000) == _lib.FLK_E_INVALID              # row shorter than 3*H*D
     assert call(rs=9220) == _lib.FLK_E_ALIGN                # row stride not a multiple of 8
     assert call(q=FAKE + 4) == _lib.FLK_E_ALIGN
@@ -367,6 +368,10 @@ def test_w8a8_validation(lib):
     assert lib.flk_quantize_act(FAKE, 3076, FAKE, 8, 3076, FAKE, FAKE, None) == _lib.FLK_E_UNSUPPORTED
     assert lib.flk_quantize_act(FAKE, 16384, FAKE, 8, 16384, FAKE, FAKE, None) == _lib.FLK_E_UNSUPPORTED
     assert lib.flk_quantize_weight(FAKE, 9216, FAKE, 3000, 9216, FAKE, FAKE, None) == _lib.FLK_E_UNSUPPORTED
+    # row / column counts whose last block's index would pass the int range
+    assert lib.flk_quantize_act(FAKE, 3072, FAKE, 2 ** 31 - 2, 3072, FAKE, FAKE, None) == _lib.FLK_E_INVALID
+    assert lib.flk_quantize_weight(FAKE, 2 ** 31 - 8, FAKE, 3072, 2 ** 31 - 8, FAKE, FAKE, None) == \
+        _lib.FLK_E_INVALID
     assert lib.flk_absmax_rows(FAKE, 4, 12, 12, FAKE, None) == _lib.FLK_E_ALIGN
     assert lib.flk_absmax_cols(FAKE, 4, 16, 8, 0, FAKE, None) == _lib.FLK_E_INVALID
     assert lib.flk_smooth_factors(FAKE, FAKE, -1, FAKE, FAKE, None) == _lib.FLK_E_INVALID
