@@ -99,6 +99,37 @@ def test_attend_rounds_launch_equals_one_head_at_a_time(device, batch, heads, le
                    P.attend_bounded(*(to_np(t[sl]) for t in (q, k, v))))
 
 
+@pytest.mark.parametrize("batch,heads,length,kernel", [
+    (1, 16, 4096, "attend_kernel"),           # exactly 256 tiles of 256 queries: one round
+    (1, 16, 4097, "attend_rounds_kernel"),    # one tile per head more: the rounds launch
+    (1, 11, 4608, "attend_kernel"),           # one round of 256-query tiles, not of 192
+    (1, 10, 4608, "attend_tile192_kernel"),   # one round with either tiling
+    (1, 28, 4608, "attend_kernel"),           # leftover needs more than one round of 192-query tiles
+])
+def test_attend_launch_boundaries_equal_one_head_at_a_time(device, batch, heads, length, kernel):
+    """Shapes on either side of flk_attend's tiling choices take the kernel it names, and every
+    head equals the same head launched alone, bit for bit."""
+    assert _lib.attend_kernel_name(batch, heads, length) == kernel
+    q, k, v = prepped_case(batch, heads, length, seed=60 + heads)
+    got = run_attend(q, k, v, device, splits=1)
+    for h in range(heads):
+        one = run_attend(*(t[:, h:h + 1] for t in (q, k, v)), device, splits=1)
+        assert np.array_equal(got[:, h:h + 1].view(np.uint32), one.view(np.uint32)), (kernel, h)
+
+
+def test_attend_long_single_head_same_in_every_tiling(device):
+    """One head of 65537 tokens (257 tiles of 256 queries: the rounds launch, its leftover
+    segments inside that one head) equals itself batched twice (514 tiles, another split into
+    rounds and leftover), bit for bit."""
+    length = 65537
+    assert _lib.attend_kernel_name(1, 1, length) == "attend_rounds_kernel"
+    q, k, v = prepped_case(1, 1, length, seed=65)
+    one = run_attend(q, k, v, device, splits=1)
+    two = run_attend(*(t.expand(2, -1, -1, -1) for t in (q, k, v)), device, splits=1)
+    for b in range(2):
+        assert np.array_equal(two[b:b + 1].view(np.uint32), one.view(np.uint32)), b
+
+
 def test_attend_random_shapes_every_launch_equals_one_head_at_a_time(device):
     """Seeded random shapes, each launched whole (flk_attend picks 256-query tiles, 192-query
     tiles or the rounds launch; the name it reports is checked against the three) and one head
