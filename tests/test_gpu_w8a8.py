@@ -166,12 +166,15 @@ def test_gemm_tails_bit_exact(device, m, k, n):
     assert_bits_equal(y, Q.rescale(acc_want, a, ws), f"y {m}x{k}x{n}")
 
 
-@pytest.mark.parametrize("m,n", [(4352, 9216), (3840, 9216), (4100, 9000), (2600, 9216), (6000, 6144)])
+@pytest.mark.parametrize("m,n", [(4352, 9216), (3840, 9216), (4100, 9000), (2600, 9216), (6000, 6144),
+                                 (4096, 4096), (4097, 4096), (4096, 4100), (8192, 8192), (8193, 8192)])
 def test_gemm_rounds_order_bit_exact(device, m, n):
     """Grids of more than one round (the Klein QKV widths): whole rounds of 256 x 256 tiles,
     then the tiles left over cut into 192-token tiles, runs of one channel tile starting and
-    ending between token tiles, the last tile of a run cut short.  Every int32 product and
-    bf16 output against the oracle (K = 128 keeps the float64 oracle product quick)."""
+    ending between token tiles, the last tile of a run cut short; and around the choice: exactly
+    one round (256 tiles), one tile row or column more, whole rounds with nothing left over,
+    and those plus one row.  Every int32 product and bf16 output against the oracle (K = 128
+    keeps the float64 oracle product quick)."""
     k = 128
     rng = np.random.default_rng(m + n)
     xq = rng.integers(-127, 128, (m, k), dtype=np.int8)
