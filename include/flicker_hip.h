@@ -10,6 +10,8 @@
  *   - Return value: FLK_OK (0) on success, a negative FLK_E_* code for an argument
  *     the kernel cannot take (checked before anything is launched), or a positive
  *     hipError_t if the launch itself failed.  flk_status_string() names each code.
+ *   - Lengths, token and channel counts are `int`; one within a tile (at most 256) of
+ *     INT32_MAX is FLK_E_INVALID, since the kernels index whole tiles in 32 bits.
  */
 #ifndef FLICKER_HIP_H
 #define FLICKER_HIP_H
