@@ -252,3 +252,24 @@ def test_double_attention_with_position_ids(device):
         out.append(modules.double_attention(*dev(txt, img), dev(qs_t, ks_t), dev(qs_i, ks_i), src, heads))
     torch.cuda.synchronize()
     assert torch.equal(out[0][0], out[1][0]) and torch.equal(out[0][1], out[1][1])
+
+
+def test_qk_prep_random_shapes(device):
+    """Seeded random shapes (batch, ragged length, any head count, so every heads-per-group
+    variant; gains; bf16 or f32 scales): the position-id form equals the table form bit for
+    bit, and both hold the oracle gate."""
+    rng = np.random.default_rng(31)
+    for trial in range(8):
+        batch, length, heads = int(rng.integers(1, 4)), int(rng.integers(1, 700)), int(rng.integers(1, 26))
+        gain = float(rng.choice([1.0, 1 / math.sqrt(128), 0.37]))
+        f32 = trial % 3 == 2
+        label = f"random B{batch} L{length} H{heads} gain{gain:.4f} {'f32' if f32 else 'bf16'} scales"
+        print(label, flush=True)
+        qkv, qs, ks, ids = make_case(batch, length, heads, seed=300 + trial,
+                                     scale_dtype=torch.float32 if f32 else torch.bfloat16)
+        via_ids, via_tables, lanes = _ids_and_tables_paths(device, qkv, qs, ks, ids, heads, gain)
+        for name, a, b in zip("qkv", via_ids, via_tables):
+            assert torch.equal(a, b), f"{label}: {name} of the ids form differs from the table form"
+        want = P.qk_prep_fused(to_np(qkv), to_np(qs), to_np(ks), lanes, heads, scale_is_bf16=not f32,
+                               return_normed=True)
+        check_qkv(label, via_tables, want, gain)
