@@ -314,6 +314,33 @@ def test_fused_projection_qk_prep_bit_exact(device, batch, length, heads, k, sca
         assert bad == 0, f"{name}: {bad} of {a.numel()} elements differ"
 
 
+def test_fused_projection_random_shapes_bit_exact(device):
+    """Seeded random projections feeding qk_prep (batches whose entries wrap inside token
+    tiles, ragged lengths, 1-24 heads, k up to 384, both scale types, gains; alternately
+    within and past one round of tiles), each equal to the GEMM followed by qk_prep, bit
+    for bit."""
+    rng = np.random.default_rng(91)
+    for trial in range(6):
+        while True:   # odd trials past one round of 256 x 256 tiles (the rounds order)
+            batch, length = int(rng.integers(1, 5)), int(rng.integers(1, 3000))
+            heads, k = int(rng.integers(1, 25)), 128 * int(rng.integers(1, 4))
+            tiles = -(-batch * length // 256) * -(-3 * heads * 128 // 256)
+            if (256 < tiles <= 700) if trial % 2 else (tiles <= 256):
+                break
+        scale_dtype = torch.float32 if trial % 2 else torch.bfloat16
+        gain = float(rng.choice([1.0, 128 ** -0.5, 0.3]))
+        label = f"B{batch} L{length} H{heads} k{k} {scale_dtype} gain{gain:.4f}"
+        print(label, flush=True)
+        x, qw, qs, ks, freqs, kernels = _fused_case(device, batch, length, heads, k, scale_dtype, gain,
+                                                    seed=900 + trial)
+        want = kernels.qk_prep(w8a8.linear(x, qw), qs, ks, freqs, heads, rows=length)
+        got = w8a8.qk_prep(x, qw, qs, ks, freqs, heads)
+        torch.cuda.synchronize()
+        for name, a, b in zip("qkv", got, want):
+            bad = int((a.view(torch.int16) != b.view(torch.int16)).sum())
+            assert bad == 0, f"{label} {name}: {bad} of {a.numel()} elements differ"
+
+
 def test_fused_projection_accepts_position_ids(device):
     """w8a8.qk_prep with PositionIds equals the table form (the lanes are built from the ids)."""
     from flicker_amd import rope
