@@ -278,7 +278,7 @@ def vendor_leg(w, qkv_sets, attend_us, gemm_us, args, timed, dev) -> dict:
 
     def leg(name, fn):
         # A comparison leg never costs the bench line: a library that fails here (no kernel
-        # for this build or shape) is recorded as such.
+        # in the installed torch for this shape) is recorded as such.
         try:
             out[name] = fn()
         except Exception as e:  # noqa: BLE001
