@@ -287,3 +287,26 @@ def test_attend_key_split_long_sequence_matches_unsplit(device):
     diff = np.abs(split.astype(np.float64) - one)
     assert np.all(diff <= 2 * np.abs(one) * 2.0 ** -8 + 1e-6)
     assert np.mean(diff > 0) <= 0.01
+
+
+def test_attend_key_split_random_small_grids(device):
+    """Seeded random small grids (fewer than 192 tiles of 256 queries), each on the range count
+    flk_attend_plan picks: within one bf16 ulp of the one-pass kernel on at most 1% of
+    elements, and at the tight oracle gate where the oracle is quick."""
+    rng = np.random.default_rng(512)
+    for trial in range(6):
+        while True:
+            batch, heads, length = int(rng.integers(1, 3)), int(rng.integers(1, 5)), int(rng.integers(200, 3000))
+            planned, _ = _lib.attend_plan(batch, heads, length)
+            if planned > 1:
+                break
+        label = f"split {planned} B{batch} H{heads} L{length}"
+        print(label, flush=True)
+        q, k, v = prepped_case(batch, heads, length, seed=700 + trial)
+        got = run_attend(q, k, v, device)
+        one = run_attend(q, k, v, device, 1)
+        diff = np.abs(got.astype(np.float64) - one)
+        assert np.all(diff <= 2 * np.abs(one) * 2.0 ** -8 + 1e-6), label
+        assert np.mean(diff > 0) <= 0.01, label
+        if length <= 1200:
+            tight_gate(label, got, P.attend_bounded(to_np(q), to_np(k), to_np(v)))
