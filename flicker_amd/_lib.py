@@ -23,6 +23,7 @@ SIGNATURES = {
     "flk_status_string": (ctypes.c_char_p, [_i]),
     "flk_qk_prep": (_i, [_p, _i64, _i64, _p, _p, _i64, _p, _p, _i, _f, _i, _i, _i, _i,
                          _p, _p, _p, _i64, _i64, _p]),
+    "flk_qk_prep_f32": (_i, [_p, _i64, _i64, _p, _p, _i64, _p, _p, _i, _i, _i, _i, _p, _p, _p, _i64, _i64, _p]),
     "flk_qk_prep_ids": (_i, [_p, _i64, _i64, _p, _i64, _i, _ip, _f, _p, _p, _i, _f, _i, _i, _i, _i,
                              _p, _p, _p, _i64, _i64, _p]),
     "flk_attend": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _p]),

@@ -37,10 +37,12 @@ __device__ __forceinline__ void load_table8(const float* row, int lane, float ou
   out[4] = b.x; out[5] = b.y; out[6] = b.z; out[7] = b.w;
 }
 
-// RMSNorm * scale, RoPE rotation and optional gain on the 8 elements this lane holds.
-template <bool kScaleF32, bool kGain>
-__device__ __forceinline__ uint4 norm_rotate(uint4 raw, const float sc[8], const float c[8],
-                                             const float s[8], float gain) {
+// RMSNorm * scale and the RoPE rotation of the 8 elements this lane holds, in float32:
+// r = cos * y + sin * swap(y) with y = bf16(x * (1 / sqrt(mean x^2 + eps))) * scale, the
+// product rounded to bf16 for a bf16 scale and kept in float32 for a float32 one.
+template <bool kScaleF32>
+__device__ __forceinline__ void norm_rotate_f32(uint4 raw, const float sc[8], const float c[8],
+                                                const float s[8], float r[8]) {
 #pragma clang fp contract(off)
   const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
   float x[8];
@@ -61,12 +63,21 @@ __device__ __forceinline__ uint4 norm_rotate(uint4 raw, const float sc[8], const
     const float n = flk::round_bf16(x[i] * inv);
     y[i] = kScaleF32 ? n * sc[i] : flk::round_bf16(n * sc[i]);
   }
-  float r[8];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     r[2 * j] = c[2 * j] * y[2 * j] + s[2 * j] * y[2 * j + 1];
     r[2 * j + 1] = c[2 * j + 1] * y[2 * j + 1] + s[2 * j + 1] * y[2 * j];
   }
+}
+
+// RMSNorm * scale, RoPE rotation and optional gain on the 8 elements this lane holds,
+// rounded to bf16 once at the end.
+template <bool kScaleF32, bool kGain>
+__device__ __forceinline__ uint4 norm_rotate(uint4 raw, const float sc[8], const float c[8],
+                                             const float s[8], float gain) {
+#pragma clang fp contract(off)
+  float r[8];
+  norm_rotate_f32<kScaleF32>(raw, sc, c, s, r);
   if constexpr (kGain) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) r[i] = gain * r[i];

@@ -88,7 +88,16 @@ __device__ __forceinline__ void store16(uint16_t* p, uint4 v) {
   }
 }
 
-template <bool kScaleF32, bool kGain, int kHeads>
+// 8 float32 values of a head row (32 bytes per lane) for the float32 outputs of the plain
+// branch; the default cache policy, as for the bf16 stores.
+__device__ __forceinline__ void store_f32x8(float* p, const float r[8]) {
+  reinterpret_cast<float4*>(p)[0] = make_float4(r[0], r[1], r[2], r[3]);
+  reinterpret_cast<float4*>(p)[1] = make_float4(r[4], r[5], r[6], r[7]);
+}
+
+// kOutF32: q and k are stored as float32 (no gain, no final rounding): the plain branch of
+// qkv_prep with float32 scales (flk_qk_prep_f32); q_out / k_out then point at floats.
+template <bool kScaleF32, bool kGain, int kHeads, bool kOutF32 = false>
 __global__ __launch_bounds__(kThreads) void qk_prep_kernel(
     const uint16_t* __restrict__ qkv, int64_t batch_stride, int64_t row_stride, RopeSource rope,
     const void* __restrict__ q_scale, const void* __restrict__ k_scale, float q_gain,
@@ -118,8 +127,16 @@ __global__ __launch_bounds__(kThreads) void qk_prep_kernel(
   for (int i = 0; i < kHeads; ++i) {
     const int64_t o =
         (((int64_t)b * num_heads + h0 + i) * out_length + out_offset + t) * kHeadDim + lane * 8;
-    store16(q_out + o, flk::norm_rotate<kScaleF32, kGain>(rq[i], qs, c, s, q_gain));
-    store16(k_out + o, flk::norm_rotate<kScaleF32, false>(rk[i], ks, c, s, 1.0f));
+    if constexpr (kOutF32) {
+      float r[8];
+      flk::norm_rotate_f32<kScaleF32>(rq[i], qs, c, s, r);
+      store_f32x8(reinterpret_cast<float*>(q_out) + o, r);
+      flk::norm_rotate_f32<kScaleF32>(rk[i], ks, c, s, r);
+      store_f32x8(reinterpret_cast<float*>(k_out) + o, r);
+    } else {
+      store16(q_out + o, flk::norm_rotate<kScaleF32, kGain>(rq[i], qs, c, s, q_gain));
+      store16(k_out + o, flk::norm_rotate<kScaleF32, false>(rk[i], ks, c, s, 1.0f));
+    }
     store16(v_out + o, rv[i]);
   }
 }
@@ -226,8 +243,11 @@ struct Launch {
 #define FLK_QK_IDS_ROUNDS 2
 #endif
 
+// Launches the kernel built for `heads_per_group` heads per 16-lane group (the grid's y size
+// is num_heads / heads_per_group); FLK_E_UNSUPPORTED, with nothing launched, for a count that
+// has no kernel (a forced tuning knob), so the grid and the kernel always agree.
 template <bool kScaleF32, bool kGain, bool kIds>
-void launch(int heads_per_group, dim3 grid, hipStream_t stream, const Launch& a) {
+int launch(int heads_per_group, dim3 grid, hipStream_t stream, const Launch& a) {
 #define FLK_QK_ARGS                                                                                \
   a.qkv, a.batch_stride, a.row_stride, a.rope, a.q_scale, a.k_scale, a.q_gain, a.length, a.num_heads, \
       a.q, a.k, a.v, a.out_length, a.out_offset
@@ -235,25 +255,28 @@ void launch(int heads_per_group, dim3 grid, hipStream_t stream, const Launch& a)
   hipLaunchKernelGGL((qk_prep_kernel<kScaleF32, kGain, NH>), grid, dim3(kThreads), 0, stream, FLK_QK_ARGS)
 #define FLK_QK_IDS(NH, R) \
   hipLaunchKernelGGL((qk_prep_ids_kernel<kScaleF32, kGain, NH, R>), grid, dim3(kThreads), 0, stream, FLK_QK_ARGS)
+  int status = FLK_OK;
   if constexpr (kIds) {
     // heads_per_group = heads per round x rounds
-    if (heads_per_group % (2 * FLK_QK_IDS_ROUNDS) == 0 && heads_per_group == 2 * FLK_QK_IDS_ROUNDS)
-      FLK_QK_IDS(2, FLK_QK_IDS_ROUNDS);
+    if (heads_per_group == 2 * FLK_QK_IDS_ROUNDS) FLK_QK_IDS(2, FLK_QK_IDS_ROUNDS);
     else if (heads_per_group == 2) FLK_QK_IDS(2, 1);
     else if (heads_per_group == 3) FLK_QK_IDS(3, 1);
-    else FLK_QK_IDS(1, 1);
+    else if (heads_per_group == 1) FLK_QK_IDS(1, 1);
+    else status = FLK_E_UNSUPPORTED;
   } else {
     switch (heads_per_group) {
       case 6: FLK_QK_LAUNCH(6); break;
       case 4: FLK_QK_LAUNCH(4); break;
       case 3: FLK_QK_LAUNCH(3); break;
       case 2: FLK_QK_LAUNCH(2); break;
-      default: FLK_QK_LAUNCH(1); break;
+      case 1: FLK_QK_LAUNCH(1); break;
+      default: status = FLK_E_UNSUPPORTED; break;
     }
   }
 #undef FLK_QK_IDS
 #undef FLK_QK_LAUNCH
 #undef FLK_QK_ARGS
+  return status;
 }
 
 // Checks shared by both entry points: FLK_OK = launch, kEmpty = nothing to do (an empty
@@ -285,14 +308,10 @@ template <bool kIds>
 int dispatch(int hpg, int batch, int scale_is_f32, hipStream_t stream, const Launch& a) {
   const dim3 grid((unsigned)(((int64_t)a.length + kTokensPerBlock - 1) / kTokensPerBlock), a.num_heads / hpg, batch);
   const bool gain = a.q_gain != 1.0f;
-  if (scale_is_f32) {
-    if (gain) launch<true, true, kIds>(hpg, grid, stream, a);
-    else launch<true, false, kIds>(hpg, grid, stream, a);
-  } else {
-    if (gain) launch<false, true, kIds>(hpg, grid, stream, a);
-    else launch<false, false, kIds>(hpg, grid, stream, a);
-  }
-  return flk_launch_status();
+  int st;
+  if (scale_is_f32) st = gain ? launch<true, true, kIds>(hpg, grid, stream, a) : launch<true, false, kIds>(hpg, grid, stream, a);
+  else st = gain ? launch<false, true, kIds>(hpg, grid, stream, a) : launch<false, false, kIds>(hpg, grid, stream, a);
+  return st != FLK_OK ? st : flk_launch_status();
 }
 
 // Heads per 16-lane group.  With tables, two measured best at the Klein shapes (6 loads in
@@ -339,6 +358,39 @@ extern "C" int flk_qk_prep(const void* qkv, int64_t qkv_batch_stride, int64_t qk
   a.out_offset = out_offset;
   return dispatch<false>(heads_per_group(num_heads, false, FLK_QK_HPG), batch, scale_is_f32,
                          static_cast<hipStream_t>(stream), a);
+}
+
+extern "C" int flk_qk_prep_f32(const void* qkv, int64_t qkv_batch_stride, int64_t qkv_row_stride,
+                               const float* cos, const float* sin, int64_t table_row_stride,
+                               const float* q_scale, const float* k_scale, int batch, int length,
+                               int num_heads, int head_dim, float* q_out, float* k_out, void* v_out,
+                               int64_t out_length, int64_t out_offset, void* stream) {
+  const int st = check_common(qkv, qkv_batch_stride, qkv_row_stride, q_scale, k_scale, batch,
+                              length, num_heads, head_dim, q_out, k_out, v_out, out_length, out_offset);
+  if (st != FLK_OK) return st == kEmpty ? FLK_OK : st;
+  if (table_row_stride < head_dim || !cos || !sin) return FLK_E_INVALID;
+  if (table_row_stride % 4 || !flk_host_aligned(cos, 16) || !flk_host_aligned(sin, 16))
+    return FLK_E_ALIGN;
+  RopeSource rope{};
+  rope.cos = cos;
+  rope.sin = sin;
+  rope.table_stride = table_row_stride;
+  const int hpg = num_heads % 2 == 0 ? 2 : 1;
+  const dim3 grid((unsigned)(((int64_t)length + kTokensPerBlock - 1) / kTokensPerBlock), num_heads / hpg, batch);
+  const hipStream_t hs = static_cast<hipStream_t>(stream);
+  const uint16_t* x = static_cast<const uint16_t*>(qkv);
+  uint16_t* qo = reinterpret_cast<uint16_t*>(q_out);
+  uint16_t* ko = reinterpret_cast<uint16_t*>(k_out);
+  uint16_t* vo = static_cast<uint16_t*>(v_out);
+  if (hpg == 2)
+    hipLaunchKernelGGL((qk_prep_kernel<true, false, 2, true>), grid, dim3(kThreads), 0, hs, x, qkv_batch_stride,
+                       qkv_row_stride, rope, q_scale, k_scale, 1.0f, length, num_heads, qo, ko, vo, out_length,
+                       out_offset);
+  else
+    hipLaunchKernelGGL((qk_prep_kernel<true, false, 1, true>), grid, dim3(kThreads), 0, hs, x, qkv_batch_stride,
+                       qkv_row_stride, rope, q_scale, k_scale, 1.0f, length, num_heads, qo, ko, vo, out_length,
+                       out_offset);
+  return flk_launch_status();
 }
 
 extern "C" int flk_qk_prep_ids(const void* qkv, int64_t qkv_batch_stride, int64_t qkv_row_stride,

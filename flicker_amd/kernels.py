@@ -122,7 +122,11 @@ def _id_args(pos: PositionIds, length: int, head_dim: int):
     return ids if ids.stride(1) == 1 else ids.contiguous()
 
 
-def _launch_qk_prep(qkv, q_scale, k_scale, freqs, num_heads: int, out, out_offset: int):
+def _launch_qk_prep(qkv, q_scale, k_scale, freqs, num_heads: int, out, out_offset: int,
+                    qk_f32: bool = False):
+    """qk_prep's launch.  ``qk_f32``: the plain branch of qkv_prep with float32 scales
+    (modules.py:78-80, where rms_norm's product and apply_rope's result stay float32): q and
+    k come out float32, unrounded and without a query gain (flk_qk_prep_f32); v stays bf16."""
     batch, length, width = qkv.shape
     head_dim = width // (3 * num_heads)
     if 3 * num_heads * head_dim != width:
@@ -145,6 +149,9 @@ def _launch_qk_prep(qkv, q_scale, k_scale, freqs, num_heads: int, out, out_offse
         raise ValueError(f"q_scale / k_scale must hold {head_dim} values")
     if q_scale.dtype != k_scale.dtype or q_scale.dtype not in (torch.bfloat16, torch.float32):
         raise TypeError("q_scale and k_scale must share one dtype, bfloat16 or float32")
+    if qk_f32 and (q_scale.dtype != torch.float32 or isinstance(freqs, PositionIds) or q_gain != 1.0):
+        raise ValueError("float32 q / k outputs are the plain branch's: float32 scales, lane tables, gain 1")
+    qk_dtype = torch.float32 if qk_f32 else torch.bfloat16
     qkv = _dense_rows(qkv)
     q_scale = q_scale.reshape(-1).contiguous()
     k_scale = k_scale.reshape(-1).contiguous()
@@ -153,21 +160,30 @@ def _launch_qk_prep(qkv, q_scale, k_scale, freqs, num_heads: int, out, out_offse
         if out_offset:
             raise ValueError("out_offset needs out=(q, k, v)")
         shape = (batch, num_heads, length, head_dim)
-        out = tuple(torch.empty(shape, dtype=torch.bfloat16, device=qkv.device) for _ in range(3))
+        out = tuple(torch.empty(shape, dtype=dt, device=qkv.device) for dt in (qk_dtype, qk_dtype, torch.bfloat16))
         out_length = length
     else:
         out = tuple(out)
         if len(out) != 3:
             raise ValueError("out must be a (q, k, v) triple")
         out_length = out[0].shape[2]
-        for t in out:
+        for t, dt in zip(out, (qk_dtype, qk_dtype, torch.bfloat16)):
             _on_gpu("out", t)
-            if (t.dtype != torch.bfloat16 or t.dim() != 4 or t.shape[0] != batch or t.shape[1] != num_heads
+            if (t.dtype != dt or t.dim() != 4 or t.shape[0] != batch or t.shape[1] != num_heads
                     or t.shape[3] != head_dim or t.shape[2] != out_length or not t.is_contiguous()):
-                raise ValueError("out tensors must be contiguous bf16 (B, H, L_out, D) of one shape")
+                raise ValueError(f"out tensors must be contiguous (B, H, L_out, D) of one shape, q and k "
+                                 f"{qk_dtype}, v bfloat16")
         if out_offset < 0 or out_offset + length > out_length:
             raise ValueError(f"out_offset {out_offset} + L {length} exceeds the output length {out_length}")
 
+    if qk_f32:
+        cos, sin = rope
+        _lib.run("flk_qk_prep_f32", (qkv, cos, sin, q_scale, k_scale, *out),
+                 qkv.data_ptr(), qkv.stride(0), qkv.stride(1), cos.data_ptr(), sin.data_ptr(), cos.stride(0),
+                 q_scale.data_ptr(), k_scale.data_ptr(), batch, length, num_heads, head_dim,
+                 out[0].data_ptr(), out[1].data_ptr(), out[2].data_ptr(), out_length, out_offset,
+                 _lib.stream_of(qkv))
+        return out
     common = (q_scale.data_ptr(), k_scale.data_ptr(), int(q_scale.dtype == torch.float32), float(q_gain),
               batch, length, num_heads, head_dim, out[0].data_ptr(), out[1].data_ptr(), out[2].data_ptr(),
               out_length, out_offset, _lib.stream_of(qkv))

@@ -37,23 +37,30 @@ def qkv_prep(qkv, q_scale, k_scale, pe, freqs: Freqs | PositionIds | None, num_h
     no query gain.  Both branches run the one HIP kernel: the plain branch's lane tables are
     built from ``pe`` at gain 1 (lane_pair), whose rotation is bit-identical to apply_rope's
     2x2 form.  ``pe`` is (B_pe, 1, L, D/2, 2, 2); with B_pe > 1 each batch element is
-    rotated by its own table, as apply_rope broadcasts it."""
+    rotated by its own table, as apply_rope broadcasts it.
+
+    The plain branch's output dtype follows the reference's promotion: with bfloat16 scales q
+    and k are bfloat16; with float32 scales rms_norm's bf16(normed) * scale is float32
+    (nn.py:27) and apply_rope casts its float32 rotation back to that dtype (rope.py:28), so
+    q and k are float32, unrounded (flk_qk_prep_f32).  v is the bfloat16 split either way."""
     if freqs is not None and row_tile(qkv.shape[1]) is not None:
         return _launch_qk_prep(qkv, q_scale, k_scale, freqs, num_heads, out, out_offset)
     if pe is None:
         raise ValueError(f"qkv_prep: L={qkv.shape[1]} has no row tile (or freqs is None), so the plain "
                          "branch needs pe")
+    qk_f32 = q_scale.dtype == torch.float32
     if pe.dim() < 6 or pe.shape[0] == 1:
-        return _launch_qk_prep(qkv, q_scale, k_scale, lane_pair(pe, 1.0), num_heads, out, out_offset)
+        return _launch_qk_prep(qkv, q_scale, k_scale, lane_pair(pe, 1.0), num_heads, out, out_offset, qk_f32)
     batch = qkv.shape[0]
     if pe.shape[0] != batch:
         raise ValueError(f"pe batch {pe.shape[0]} does not broadcast against qkv batch {batch}")
     if out is None:
         shape = (batch, num_heads, qkv.shape[1], qkv.shape[2] // (3 * num_heads))
-        out = tuple(torch.empty(shape, dtype=torch.bfloat16, device=qkv.device) for _ in range(3))
+        qk_dtype = torch.float32 if qk_f32 else torch.bfloat16
+        out = tuple(torch.empty(shape, dtype=dt, device=qkv.device) for dt in (qk_dtype, qk_dtype, torch.bfloat16))
     for b in range(batch):
         _launch_qk_prep(qkv[b:b + 1], q_scale, k_scale, lane_pair(pe[b:b + 1], 1.0), num_heads,
-                        tuple(t[b:b + 1] for t in out), out_offset)
+                        tuple(t[b:b + 1] for t in out), out_offset, qk_f32)
     return tuple(out)
 
 

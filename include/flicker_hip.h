@@ -57,6 +57,24 @@ int flk_qk_prep(const void* qkv, int64_t qkv_batch_stride, int64_t qkv_row_strid
                 void* stream);
 
 /*
+ * The plain branch of qkv_prep with float32 norm scales (src/flicker/modules.py:78-80: heads,
+ * qk_norm, apply_rope).  There rms_norm's bf16(x * rsqrt) * scale promotes to float32
+ * (src/flicker/nn.py:27) and apply_rope casts its float32 rotation back to that dtype
+ * (src/flicker/rope.py:28), so q and k come out float32: the rotation of the float32 product,
+ * with no rounding after it and no query gain.  v is the bf16 copy, as in flk_qk_prep.
+ *   q_scale, k_scale (head_dim,) float32
+ *   cos, sin   lane tables of the plain branch's rope table at gain 1 (kernels.lane_pair layout)
+ *   q_out, k_out (batch, num_heads, out_length, head_dim) float32; v_out bf16 of that shape
+ * Every other argument as flk_qk_prep.  With bf16 scales the plain branch's q and k are
+ * bf16 and flk_qk_prep at q_gain 1 computes them.
+ */
+int flk_qk_prep_f32(const void* qkv, int64_t qkv_batch_stride, int64_t qkv_row_stride,
+                    const float* cos, const float* sin, int64_t table_row_stride,
+                    const float* q_scale, const float* k_scale, int batch, int length,
+                    int num_heads, int head_dim, float* q_out, float* k_out, void* v_out,
+                    int64_t out_length, int64_t out_offset, void* stream);
+
+/*
  * flk_qk_prep with the RoPE lanes computed in the kernel from position ids instead of read
  * from cos / sin tables: the fused form of qk_prep(qkv, ..., lane_pair(embed_nd(ids))),
  * i.e. kernels.qk_prep (src/flicker/kernels.py:57-91) over rope.embed_nd

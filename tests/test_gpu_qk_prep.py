@@ -129,6 +129,42 @@ def test_qk_prep_f32_scales(device):
     check_qkv("f32 scales", got, want, tables.q_gain)
 
 
+@pytest.mark.parametrize("batch,length,pe_batch", [(1, 100, 1), (2, 257, 2)])
+def test_qkv_prep_plain_branch_f32_scales(device, batch, length, pe_batch):
+    """The plain branch (modules.py:78-80) with float32 norm scales returns float32 q and k:
+    rms_norm's bf16(normed) * scale promotes to float32 (nn.py:27) and apply_rope casts the
+    float32 rotation back to that dtype (rope.py:28), so nothing is rounded after the normed
+    value; v stays the bf16 split.  Against oracle.path.qk_prep_plain(..., scale_is_bf16=False):
+    v bit-exact; q and k equal except where the kernel's float32 mean of squares flips the
+    intermediate bf16(x * rsqrt) by one ulp, each such difference within that flip carried
+    through the rotation."""
+    qkv, qs, ks, ids = make_case(batch, length, 24, seed=1300 + length, scale_dtype=torch.float32)
+    if pe_batch > 1:
+        g = np.random.default_rng(length)
+        ids = np.stack([ids] + [g.integers(0, 128, ids.shape).astype(np.float32) for _ in range(pe_batch - 1)])
+    pe = P.embed_nd(ids)
+    assert P.row_tile(length) is None, "the case must take the plain branch"
+    got = modules.qkv_prep(qkv.to(device), qs.to(device), ks.to(device), torch.from_numpy(pe).to(device),
+                           gpu_freqs(P.lane_pair(pe[:1], 1 / math.sqrt(D)), device), 24)
+    torch.cuda.synchronize()
+    assert got[0].dtype == got[1].dtype == torch.float32 and got[2].dtype == torch.bfloat16
+    wq, wk, wv = P.qk_prep_plain(to_np(qkv), to_np(qs), to_np(ks), pe, 24, scale_is_bf16=False)
+    assert wq.dtype == np.float32
+    assert np.array_equal(to_np(got[2]), wv), "v is not a bit-exact copy"
+    for name, g, w, sc in (("q", got[0], wq, to_np(qs)), ("k", got[1], wk, to_np(ks))):
+        g = g.cpu().numpy()
+        diff = np.abs(g.astype(np.float64) - w.astype(np.float64))
+        # one flip of the normed bf16 value n in element i or its pair partner moves the output by at
+        # most ulp(n_i) |sc_i| + ulp(n_pair) |sc_pair| (|cos|, |sin| <= 1); |n| < 16 for unit-RMS rows
+        flip = np.float64(2.0 ** -8 * 16) * np.abs(sc).max() * 2
+        mismatch = float((diff > 0).mean())
+        print(f"plain f32 B{batch} L{length} {name}: mismatch {mismatch:.3g} max diff {diff.max():.3g}")
+        assert mismatch <= 1e-4, (name, mismatch)
+        assert diff.max() <= flip, (name, diff.max())
+    rms = np.sqrt((got[0].cpu().numpy().astype(np.float64) ** 2).mean(-1)).mean()
+    assert abs(rms - 1.0) < 0.05, rms   # no query gain on the plain branch
+
+
 def test_qk_prep_gain_one_equals_plain_path(device):
     """At q_gain = 1 the fused kernel computes the plain-XLA branch (modules.py:78-80)."""
     qkv, qs, ks, ids = make_case(2, 256, 24, seed=11)

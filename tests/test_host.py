@@ -188,6 +188,29 @@ def test_qk_prep_validation(lib):
     assert call(l=0) == _lib.FLK_OK
 
 
+def test_qk_prep_f32_validation(lib):
+    """flk_qk_prep_f32 (the plain branch with float32 scales) shares flk_qk_prep's checks:
+    head width, strides, alignment, table arguments; empty problems launch nothing."""
+    f = lib.flk_qk_prep_f32
+    hd = 3 * 24 * 128
+
+    def call(**kw):
+        a = dict(qkv=FAKE, bs=100 * hd, rs=hd, cos=FAKE, sin=FAKE, ts=128, qs=FAKE, ks=FAKE, b=1, n=100, h=24,
+                 d=128, q=FAKE, k=FAKE, v=FAKE, ol=100, oo=0)
+        a.update(kw)
+        return f(a["qkv"], a["bs"], a["rs"], a["cos"], a["sin"], a["ts"], a["qs"], a["ks"], a["b"], a["n"],
+                 a["h"], a["d"], a["q"], a["k"], a["v"], a["ol"], a["oo"], None)
+
+    assert call(d=64) == _lib.FLK_E_UNSUPPORTED
+    assert call(rs=hd - 8) == _lib.FLK_E_INVALID
+    assert call(ts=64) == _lib.FLK_E_INVALID
+    assert call(cos=None) == _lib.FLK_E_INVALID
+    assert call(q=FAKE + 4) == _lib.FLK_E_ALIGN
+    assert call(ts=130) == _lib.FLK_E_ALIGN
+    assert call(oo=1) == _lib.FLK_E_INVALID
+    assert call(n=0) == _lib.FLK_OK and call(b=0) == _lib.FLK_OK
+
+
 def test_qk_prep_ids_validation(lib):
     f = lib.flk_qk_prep_ids
     args = dict(qkv=FAKE, bs=4608 * 9216, rs=9216, ids=FAKE, ids_rs=4, n_axes=4,
