@@ -76,6 +76,9 @@ def parse():
     ap.add_argument("--no-vendor", action="store_true",
                     help="skip the comparison legs through ROCm's libraries (torch SDPA flash, hipBLASLt GEMMs)")
     ap.add_argument("--projection", default="qkv_1024")
+    ap.add_argument("--workloads", default="klein_512,klein_1536x640,klein_2048,klein_1024_b4",
+                    help="the other Klein configurations timed after the headline one (qk_prep and attend "
+                         "legs, same method), reported under 'workloads'; empty = none")
     ap.add_argument("--cpu-reps", type=int, default=9,
                     help="timed CPU-baseline steps (after 3 warm-up steps); the p50 is reported")
     ap.add_argument("--only", choices=["step", "calibrate"], default="step",
@@ -258,6 +261,69 @@ def head_share_leg(w, qkv_heads, timed) -> dict:
     return {"heads": heads, "of_gpus": SHARE_GPUS, "splits": splits, "avg_launch_us": round(split_ms * 1e3, 2),
             "achieved": round(flops / (split_ms * 1e-3) / 1e12, 1), "unit": "TFLOP/s",
             "unsplit_us": round(plain_ms * 1e3, 2)}
+
+
+def workload_leg(name: str, kernel_timed, dev) -> dict:
+    """qk_prep and attend at another Klein configuration, timed like the headline legs: each
+    kernel alone, back to back over rotating buffer sets (more than twice the Infinity Cache),
+    after its clock settle; the smaller of eager launches and a replayed HIP graph.  For the
+    stressed batch (5% of the QKV channels x8) the load-time logit-bound check runs on the
+    norm scales and the runtime logit maximum of head 0 is compared with the bound."""
+    import torch
+
+    from flicker_amd import kernels, loader, rope, workloads
+
+    w = workloads.WORKLOADS[name]
+    qkv_cpu = workloads.make_qkv(w)
+    qs, ks = (t.to(dev) for t in workloads.make_scales(w))
+    freqs = rope.rope_lanes(workloads.make_ids(w), workloads.q_gain(w), device=dev)
+    act_bytes = qkv_cpu.numel() * 2
+    n_sets = max(2, -(-2 * INFINITY_CACHE_BYTES // (2 * act_bytes + act_bytes // 3)))
+    sets = []
+    for _ in range(n_sets):
+        out = tuple(torch.empty((w.batch, w.num_heads, w.length, w.head_dim), dtype=torch.bfloat16, device=dev)
+                    for _ in range(3))
+        sets.append((qkv_cpu.to(dev), out, torch.empty_like(out[0])))
+    del qkv_cpu
+
+    def run_qk(i):
+        qkv, out, _ = sets[i % n_sets]
+        kernels.qk_prep(qkv, qs, ks, freqs, w.num_heads, out=out)
+
+    def run_attend(i):
+        _, out, o = sets[i % n_sets]
+        kernels.attend(*out, out=o)
+
+    for i in range(n_sets):
+        run_qk(i)
+    n = max(20, min(200, int(0.2 / (w.attend_flops() / 1.2e15))))
+    qk_ms = kernel_timed(run_qk, n, f"{name}/qk_prep")
+    at_ms = kernel_timed(run_attend, n, f"{name}/attend")
+    at = w.attend_flops() / (at_ms * 1e-3) / 1e12
+    gbs = w.qk_prep_bytes() / (qk_ms * 1e-3) / 1e9
+    rec = {"config": f"B={w.batch}, {w.num_txt} text + {w.height}x{w.width} image tokens = L {w.length}, "
+                     f"{w.num_heads}x{w.head_dim} heads" + (f", {w.stress_fraction:.0%} of QKV channels x8"
+                                                            if w.stress_fraction else ""),
+           "buffer_sets": n_sets, "launches": n,
+           "attend": {"avg_launch_us": round(at_ms * 1e3, 2), "achieved": round(at, 1), "unit": "TFLOP/s",
+                      "frac": round(at / BF16_DENSE_PEAK_TFLOPS, 4), "flops_per_launch": w.attend_flops(),
+                      "kernel": " + ".join(kernels.attend_kernels(w.batch, w.num_heads, w.length))},
+           "qk_prep": {"avg_launch_us": round(qk_ms * 1e3, 2), "achieved": round(gbs, 1), "unit": "GB/s",
+                       "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_launch": w.qk_prep_bytes()}}
+    if w.stress_fraction:
+        bound = float(kernels.logit_bound(qs.float().cpu(), ks.float().cpu()))
+        qn, kn = qs.float().cpu(), ks.float().cpu()   # the same scales in every block of the stack
+        double = {f"{s}_attn.norm.{n}.scale": t.expand(5, -1) for s in ("img", "txt")
+                  for n, t in (("query_norm", qn), ("key_norm", kn))}
+        single = {"norm.query_norm.scale": qn.expand(20, -1), "norm.key_norm.scale": kn.expand(20, -1)}
+        loader.check_logit_bound({"double_blocks": double, "single_blocks": single})
+        q, k, _ = sets[0][1]
+        logits = q[0, 0].float() @ k[0, 0].float().T   # q carries the 1/sqrt(D) gain: these are attend's logits
+        rec["logit_bound"] = {"bound": round(bound, 3), "runtime_max_head0": round(float(logits.abs().max()), 3),
+                              "limit": kernels.EXP_LIMIT, "check_logit_bound": "passed"}
+    del sets
+    torch.cuda.empty_cache()
+    return rec
 
 
 def vendor_leg(w, qkv_sets, attend_us, gemm_us, args, timed, dev) -> dict:
@@ -698,6 +764,9 @@ def main() -> int:
         if "w8a8_gemm" in traffic and proj.tokens == w.batch * w.length:
             result["w8a8"]["roofline"]["traffic"] = round(traffic["w8a8_gemm"]["traffic_bytes"])
             result["w8a8"]["roofline"]["traffic_source"] = source
+    if args.workloads and args.only == "step":
+        result["workloads"] = {name: workload_leg(name, kernel_timed, dev)
+                               for name in args.workloads.split(",") if name and name != w.name}
     if not args.no_vendor and args.only == "step":
         gemm_us = result["w8a8"]["roofline"]["avg_launch_us"] if "w8a8" in result else None
         result["vendor"] = vendor_leg(w, [s[1] for s in sets], at_ms * 1e3, gemm_us, args, settled(timed), dev)
