@@ -3,8 +3,15 @@
  * flicker_amd's drop-in replacements for kelechi-c/flicker's DiT attention hot path.
  *
  * Conventions for every entry point:
- *   - The caller owns every buffer (device memory).  The library allocates nothing,
- *     keeps no state between calls and never synchronises the host.
+ *   - The caller owns every buffer (device memory).  The library allocates nothing and
+ *     never synchronises the host.  Two pieces of state outlive a call:
+ *       * flk_attend_split_static_to's fixed scratch buffer, a file-scope device array of
+ *         FLK_ATTEND_STATIC_SCRATCH_BYTES per GPU (reserved on a GPU when the library's
+ *         attend code object is loaded there, i.e. for every attend user), and the device
+ *         address of it that the first such call on a GPU looks up and caches;
+ *       * the int counters in a flk_attend_balanced_to workspace, which must be zero when a
+ *         call starts and which each call leaves zero (the workspace is the caller's, the
+ *         invariant the library's).
  *   - Work is enqueued on `stream` (a hipStream_t; NULL = the default stream).
  *   - bf16 tensors are passed as `void*` to raw 16-bit bf16 storage.
  *   - Return value: FLK_OK (0) on success, a negative FLK_E_* code for an argument
@@ -156,8 +163,10 @@ int flk_attend_split_to(const void* q, const void* k, const void* v, void* o,
  * flk_attend_split_to without a caller workspace: it allocates nothing (no hipMalloc, no
  * allocating library call).  No counterpart in the reference; it is for callers that cannot
  * allocate (code under HIP graph capture, tight serving loops, harnesses that forbid it).
- * The partials live in a fixed device buffer of FLK_ATTEND_STATIC_SCRATCH_BYTES per GPU,
- * held from the first call on that GPU until the process ends: enough for every split that
+ * The partials live in a fixed device buffer of FLK_ATTEND_STATIC_SCRATCH_BYTES per GPU, a
+ * file-scope __device__ array of the attend code object: it is reserved on a GPU as soon as
+ * the library's attend kernels are loaded there (every attend user holds it, whether or not
+ * it calls this function) and kept until the process ends.  It is enough for every split that
  * flk_attend_plan picks (at most 256 (b, h, 256-query tile, range) blocks of 133120 bytes).
  *   - A call whose workspace (as flk_attend_split_to's) would exceed the buffer returns
  *     FLK_E_SCRATCH before anything is launched; splits == 1 needs no buffer.
