@@ -162,10 +162,10 @@ _BALANCED_WORKSPACE: dict = {}
 
 def balanced_workspace(device: torch.device, stream: int, nbytes: int, counters_offset: int) -> torch.Tensor:
     """The balanced attend's workspace for one (device, stream): allocated zeroed on first use
-    and kept, since every call leaves its counters zero.  One per stream, so that calls on
-    different streams never share one.  Under graph capture a fresh workspace is taken from
-    the capture's pool and its counters are cleared by a captured fill, which every replay
-    repeats."""
+    and kept, since its hand-off counters carry each call's epoch and need no reset.  One per
+    stream, so that calls on different streams never share one.  Under graph capture a fresh
+    workspace is taken from the capture's pool and its counters are zeroed by a captured fill
+    (a fill kernel, not a memset node), so no garbage in the pool can pass for a live count."""
     if torch.cuda.is_current_stream_capturing():
         ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
         ws[counters_offset:].zero_()

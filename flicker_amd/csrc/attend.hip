@@ -68,6 +68,7 @@
 // divides.  With no running max the partial sums need no rescaling.
 
 #include <algorithm>
+#include <atomic>
 #include <mutex>
 
 #include "common.h"
@@ -692,19 +693,47 @@ __global__ __launch_bounds__(kThreads, 2) void attend_rounds_kernel(
 // at most two segments, and a leftover tile is covered by the ranges of CUs cf .. cl.
 //
 // A tile covered by one range is written directly.  Otherwise each of its pieces, when its
-// segment ends, either finds the tile's counter at pieces - 1 (every other piece published)
-// or publishes its (acc, l) partial: coherent stores to its slot, a wait until they have
-// completed, then the counter increment -- whose old value says whether it was the last.
-// The last piece sums all the pieces in CU order, ((p0 + p1) + p2) + ..., so the result does
-// not depend on the order of arrival (its own piece from registers when it is p0 or p1,
-// whose sum is the same either way; otherwise it publishes too and reads its own back), writes
-// O and resets the counter to 0 for the next launch.  No block ever waits for another.  A device-scope fence here would write back and
+// segment ends, either finds the tile's counter at pieces - 1 arrivals (every other piece
+// published) or publishes its (acc, l) partial: coherent stores to its slot, a wait until they
+// have completed, then its arrival on the counter -- whose previous count says whether it was
+// the last.  The last piece sums all the pieces in CU order, ((p0 + p1) + p2) + ..., so the
+// result does not depend on the order of arrival (its own piece from registers when it is p0
+// or p1, whose sum is the same either way; otherwise it publishes too and reads its own back)
+// and writes O.  No block ever waits for another.
+//
+// A counter holds (epoch << 8) | arrivals, the epoch a tag the host gives each call.  A value
+// with another epoch, or a count that is already complete (arrivals >= pieces: the previous
+// replay of the same captured launch), counts as no arrival, so the counters are never reset:
+// a workspace left in any state by an earlier call -- even by two calls that overlapped on it
+// -- is valid again for the next call that has it to itself.  A device-scope fence here would write back and
 // invalidate the whole L2 of the XCD for every piece, which stalls every block streaming
 // keys through that L2 (tens of microseconds per fence).
 struct XcdSplit {
   int ux0, R, r, P;
   int W;   // leftover key tiles (< 32 ntiles; the host keeps 1024 ntiles below 2^31)
 };
+
+constexpr unsigned kEpochMask = 0xFFFFFFu;   // 24-bit call tags, 8-bit arrival counts (<= 32 pieces)
+
+// Arrivals a counter value records for this call's tile of `pieces` pieces.
+__device__ __forceinline__ int arrivals_of(unsigned c, unsigned epoch, int pieces) {
+  const int n = (int)(c & 0xFFu);
+  return ((c >> 8) == epoch && n < pieces) ? n : 0;
+}
+
+// This piece's arrival: the counter becomes (epoch << 8) | (arrivals + 1); returns the arrivals
+// before it (pieces - 1: this piece is the last).  `old` is the value last read from the counter:
+// the compare-and-swap succeeds at once unless another piece arrived since, and each retry
+// starts from the value the failed swap returned.
+__device__ __forceinline__ int arrive(int* counter, unsigned epoch, int pieces, unsigned old) {
+  for (;;) {
+    const int prior = arrivals_of(old, epoch, pieces);
+    const unsigned want = (epoch << 8) | (unsigned)(prior + 1);
+    const unsigned seen = (unsigned)atomicCAS(counter, (int)old, (int)want);
+    if (seen == old) return prior;
+    old = seen;
+  }
+}
 
 __device__ __forceinline__ XcdSplit xcd_split(int units, int ntiles, int x) {
   constexpr int C = kCUs / kXcds;
@@ -754,9 +783,10 @@ __global__ __launch_bounds__(kThreads, 2) void attend_balanced_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, uint16_t* __restrict__ o, int length, int q_blocks, int units,
     int heads, int64_t o_batch_stride, int64_t o_head_stride, int64_t o_row_stride,
-    float* __restrict__ part_acc, float* __restrict__ part_l, int* __restrict__ counters) {
+    float* __restrict__ part_acc, float* __restrict__ part_l, int* __restrict__ counters, unsigned epoch) {
   __shared__ __attribute__((aligned(1024))) uint8_t smem[kSmemBytes];
   __shared__ int arrival;
+  __shared__ unsigned counter_seen;   // the counter's value when this piece checked it
   constexpr int C = kCUs / kXcds;
   const int x = blockIdx.x % kXcds, l = blockIdx.x / kXcds;   // hardware deals blocks round-robin over XCDs
   const int ntiles = (length + kBN - 1) / kBN;
@@ -797,17 +827,23 @@ __global__ __launch_bounds__(kThreads, 2) void attend_balanced_kernel(
       return (int64_t)(x * C + c) * 2 + (i - range_start(xs, c) / ntiles);
     };
     int* counter = &counters[x * C + i];
-    if (threadIdx.x == 0) arrival = __hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int pieces = others + 1;
+    if (threadIdx.x == 0) {
+      counter_seen = (unsigned)__hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      arrival = arrivals_of(counter_seen, epoch, pieces);
+    }
     __syncthreads();
     // Publish unless every other piece already has and this piece is one of the first two
     // (whose sum is the same in either order, so it can start from its registers).
     if (arrival < others || pos >= 2) {
       store_partial<true>(w, ls, part_acc, part_l, slot_of(l));
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      __syncthreads();   // every wave's stores have completed before the increment
-      if (threadIdx.x == 0) arrival = atomicAdd(counter, 1);
+      __syncthreads();   // every wave's stores have completed before the arrival
+      if (threadIdx.x == 0) arrival = arrive(counter, epoch, pieces, counter_seen);
       __syncthreads();
       if (arrival < others) continue;   // a later piece writes O
+    } else if (threadIdx.x == 0) {
+      arrive(counter, epoch, pieces, counter_seen);   // the count completes: a replay with this epoch starts afresh
     }
     // Last piece: O = ((p_cf + p_cf+1) + p_cf+2) + ..., the pieces in CU order.
     if (pos <= 1) {
@@ -817,7 +853,6 @@ __global__ __launch_bounds__(kThreads, 2) void attend_balanced_kernel(
       for (int c = cf; c <= cl; ++c) gather_partial(w.oacc, ls, c == cf, part_acc, part_l, slot_of(c));
     }
     store_o(w, ls, o, bh, heads, q0, length, o_batch_stride, o_head_stride, o_row_stride);
-    if (threadIdx.x == 0) *counter = 0;
   }
 }
 
@@ -1043,10 +1078,13 @@ extern "C" int flk_attend_balanced_to(const void* q, const void* k, const void* 
   float* part_acc = reinterpret_cast<float*>(ws);
   float* part_l = reinterpret_cast<float*>(ws + 2 * (int64_t)grid * kSlotAccBytes);
   int* counters = reinterpret_cast<int*>(ws + balanced_counters_offset(grid));
+  // This call's counter tag: 1 .. 2^24 - 1 in turn (0 is what a zeroed workspace holds).
+  static std::atomic<unsigned> next_epoch{0};
+  const unsigned epoch = next_epoch.fetch_add(1, std::memory_order_relaxed) % kEpochMask + 1;
   hipLaunchKernelGGL(attend_balanced_kernel, dim3((unsigned)grid), dim3(kThreads), 0, static_cast<hipStream_t>(stream),
                      static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
                      static_cast<uint16_t*>(o), length, (int)q_tiles(length), (int)units, heads, o_batch_stride,
-                     o_head_stride, o_row_stride, part_acc, part_l, counters);
+                     o_head_stride, o_row_stride, part_acc, part_l, counters, epoch);
   return flk_launch_status();
 }
 

@@ -9,9 +9,9 @@
  *         FLK_ATTEND_STATIC_SCRATCH_BYTES per GPU (reserved on a GPU when the library's
  *         attend code object is loaded there, i.e. for every attend user), and the device
  *         address of it that the first such call on a GPU looks up and caches;
- *       * the int counters in a flk_attend_balanced_to workspace, which must be zero when a
- *         call starts and which each call leaves zero (the workspace is the caller's, the
- *         invariant the library's).
+ *       * the int counters in a flk_attend_balanced_to workspace (the caller's memory): each
+ *         call leaves them tagged with its own epoch, a process-wide call number the library
+ *         keeps, and no later call needs them reset.
  *   - Work is enqueued on `stream` (a hipStream_t; NULL = the default stream).
  *   - bf16 tensors are passed as `void*` to raw 16-bit bf16 storage.
  *   - Return value: FLK_OK (0) on success, a negative FLK_E_* code for an argument
@@ -197,8 +197,12 @@ int flk_attend_split_static_to(const void* q, const void* k, const void* v, void
  *   - Takes every shape flk_attend_to takes; flk_attend_balanced_plan says whether it is the
  *     faster launch for a shape.
  *   - `workspace`: caller-owned, 16-byte aligned, at least flk_attend_balanced_plan's bytes.
- *     The int counters at its counters_offset must be zero before the first call that uses
- *     it (allocate it zeroed); each call leaves them zero.  Calls that share one workspace
+ *     The int counters at its counters_offset hold (epoch << 8) | arrivals, the epoch a tag
+ *     of each call (1 .. 2^24 - 1 in turn); a count from another epoch or an already complete
+ *     count is read as no arrivals, so the counters are never reset.  Allocate them zeroed
+ *     (epoch 0 is never issued); after that any state an earlier call left -- even two calls
+ *     that overlapped on the workspace, whose own results are then undefined -- is valid
+ *     for the next call that has the workspace to itself.  Calls that share one workspace
  *     must not overlap (one workspace per stream).
  *   - Other arguments as flk_attend_to.
  */
@@ -211,8 +215,8 @@ int flk_attend_balanced_to(const void* q, const void* k, const void* v, void* o,
  * Whether flk_attend_balanced_to is the faster launch for a shape (*grid = its block count,
  * 256, else 0: with fewer than 256 tiles, or a last round of tiles filling more than 5/8 of
  * the CUs, one block per tile -- or the key split -- is as fast or faster), its workspace
- * size and the byte offset of the counters that must start at zero (both independent of the
- * shape).  No device work.
+ * size and the byte offset of its hand-off counters, to be allocated zeroed (both independent
+ * of the shape).  No device work.
  */
 int flk_attend_balanced_plan(int batch, int heads, int length, int* grid, int64_t* workspace_bytes,
                              int64_t* counters_offset);
