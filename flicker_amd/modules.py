@@ -83,6 +83,10 @@ def double_attention(txt_qkv, img_qkv, txt_scales, img_scales, freqs: Freqs | Po
     they are read only by a stream whose length has no row tile (the gate's plain branch)."""
     batch, num_txt, width = txt_qkv.shape
     num_img = img_qkv.shape[1]
+    for name, length, scales in (("text", num_txt, txt_scales), ("image", num_img, img_scales)):
+        if row_tile(length) is None and scales[0].dtype == torch.float32:
+            raise TypeError(f"double_attention: the {name} stream (L={length}, no row tile) takes qkv_prep's plain "
+                            "branch, whose float32 norm scales give float32 q and k; attend takes bf16 operands only")
     head_dim = width // (3 * num_heads)
     shape = (batch, num_heads, num_txt + num_img, head_dim)
     joint = tuple(torch.empty(shape, dtype=torch.bfloat16, device=txt_qkv.device) for _ in range(3))

@@ -290,6 +290,14 @@ def test_qkv_prep_gate_host_side():
         modules.qkv_prep(qkv, torch.ones(128), torch.ones(128), pe, f, 24)
     with pytest.raises(ValueError, match="broadcast"):
         modules.qkv_prep(qkv, torch.ones(128), torch.ones(128), torch.cat([pe] * 3), f, 24)
+    # a double block whose stream takes the plain branch with float32 scales would hand attend
+    # float32 q and k: refused up front (attend takes bf16 only), before anything is launched
+    txt = torch.zeros(1, 100, 9216, dtype=torch.bfloat16)
+    img = torch.zeros(1, 512, 9216, dtype=torch.bfloat16)
+    joint = kernels.Freqs(torch.zeros(612, 128), torch.zeros(612, 128), 1 / math.sqrt(128))
+    f32, b16 = torch.ones(128), torch.ones(128, dtype=torch.bfloat16)
+    with pytest.raises(TypeError, match="text stream .* float32"):
+        modules.double_attention(txt, img, (f32, f32), (b16, b16), joint, 24)
 
 
 def test_logit_bound_and_check_match_oracle():
