@@ -87,6 +87,9 @@ def parse():
                     help="rocprofv3 --pmc output dirs of FETCH_SIZE / WRITE_SIZE runs of --only calibrate")
     ap.add_argument("--ingest-mfma", metavar="DIR",
                     help="rocprofv3 --pmc output dir of a default run with the MFMA_COUNTERS")
+    ap.add_argument("--ingest-trace", metavar="DIR",
+                    help="rocprofv3 --kernel-trace --output-format csv output dir: print its per-leg and "
+                         "all-dispatch tables (markdown)")
     return ap.parse_args()
 
 
@@ -503,8 +506,60 @@ def w8a8_leg(args, timed, dev) -> dict:
             "dtype": "int8 operands, int32 accumulate, bf16 out"}
 
 
+def _trace_rows(directory: str) -> list:
+    """(kernel, blocks, start ns, end ns) of every dispatch in a kernel trace, in start order."""
+    files = glob.glob(os.path.join(directory, "**", "*kernel_trace.csv"), recursive=True)
+    if not files:
+        raise SystemExit(f"no kernel_trace.csv under {directory}")
+    rows = []
+    for f in files:
+        for r in csv.DictReader(open(f)):
+            name = r["Kernel_Name"].replace("void ", "", 1).replace("(anonymous namespace)::", "").split("(")[0]
+            blocks = 1
+            for a in "XYZ":
+                blocks *= int(r["Grid_Size_" + a]) // max(1, int(r["Workgroup_Size_" + a]))
+            rows.append((name, blocks, int(r["Start_Timestamp"]), int(r["End_Timestamp"])))
+    rows.sort(key=lambda t: t[2])
+    return rows
+
+
+def ingest_trace(directory: str, min_run: int = 100, min_share: float = 0.002) -> str:
+    """Markdown tables of a kernel trace: each run of >= min_run consecutive dispatches of one
+    kernel and grid (a bench leg) with its mean duration and start-to-start period, then every
+    kernel and grid with its dispatch statistics and share of the summed kernel time."""
+    import statistics
+    rows = _trace_rows(directory)
+    out = ["| kernel | blocks | launches in the run | mean duration (us) | period start to start (us) |",
+           "|---|---|---|---|---|"]
+    run = []
+    for r in rows + [None]:
+        if run and (r is None or r[:2] != run[-1][:2]):
+            if len(run) >= min_run:
+                d = [(e - s) / 1e3 for _, _, s, e in run]
+                period = (run[-1][2] - run[0][2]) / (len(run) - 1) / 1e3
+                out.append(f"| `{run[0][0]}` | {run[0][1]} | {len(run)} | {sum(d) / len(d):.1f} | {period:.1f} |")
+            run = []
+        if r is not None:
+            run.append(r)
+    groups: dict = {}
+    for name, blocks, s, e in rows:
+        groups.setdefault((name, blocks), []).append((e - s) / 1e3)
+    total = sum(sum(v) for v in groups.values())
+    out += ["", "| kernel | blocks | calls | avg (us) | median (us) | min (us) | max (us) | share |",
+            "|---|---|---|---|---|---|---|---|"]
+    for (name, blocks), d in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
+        if sum(d) < min_share * total:
+            continue
+        out.append(f"| `{name}` | {blocks} | {len(d)} | {sum(d) / len(d):.1f} | {statistics.median(d):.1f} | "
+                   f"{min(d):.1f} | {max(d):.1f} | {100 * sum(d) / total:.2f}% |")
+    return "\n".join(out)
+
+
 def main() -> int:
     args = parse()
+    if args.ingest_trace:
+        print(ingest_trace(args.ingest_trace))
+        return 0
     if args.ingest_mfma:
         summary = ingest_mfma(args.ingest_mfma, args.workload)
         with open(mfma_file(args.workload), "w") as f:

@@ -385,6 +385,35 @@ def test_bench_refuses_multi_gpu():
     assert proc.returncode == 2 and "one GPU" in proc.stderr
 
 
+def test_bench_ingest_trace(tmp_path):
+    """--ingest-trace: runs of >= 100 consecutive dispatches of one kernel and grid become leg
+    rows (mean duration, start-to-start period); every kernel and grid gets a dispatch row."""
+    cols = ["Kernel_Name", "Grid_Size_X", "Grid_Size_Y", "Grid_Size_Z", "Workgroup_Size_X", "Workgroup_Size_Y",
+            "Workgroup_Size_Z", "Start_Timestamp", "End_Timestamp"]
+    rows, t = [], 0
+    # 120 launches of A (10 us each, every 12 us), 5 of B, 100 of A on another grid
+    for name, grid, count, dur in (("void (anonymous namespace)::a_kernel<1>(int)", 2560, 120, 10_000),
+                                   ("b_kernel", 256, 5, 40_000), ("void (anonymous namespace)::a_kernel<1>(int)",
+                                                                   5120, 100, 20_000)):
+        for _ in range(count):
+            rows.append([name, grid, 1, 1, 256, 1, 1, t, t + dur])
+            t += dur + 2_000
+    with open(tmp_path / "run_kernel_trace.csv", "w") as f:
+        f.write(",".join(cols) + "\n")
+        for r in rows:
+            f.write(",".join(f'"{v}"' if isinstance(v, str) else str(v) for v in r) + "\n")
+    proc = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--ingest-trace", str(tmp_path)],
+                          capture_output=True, text=True, timeout=120)
+    assert proc.returncode == 0, proc.stderr
+    lines = proc.stdout.splitlines()
+    assert "| `a_kernel<1>` | 10 | 120 | 10.0 | 12.0 |" in lines
+    assert "| `a_kernel<1>` | 20 | 100 | 20.0 | 22.0 |" in lines
+    assert not any(line.startswith("| `b_kernel` | 1 | 5 |") and line.count("|") == 6 for line in lines)
+    assert any(line.startswith("| `b_kernel` | 1 | 5 | 40.0 | 40.0 | 40.0 | 40.0 |") for line in lines)
+    share_a = [line for line in lines if line.startswith("| `a_kernel<1>` | 20 | 100 | 20.0 | 20.0 |")][0]
+    assert share_a.endswith(f"| {100 * 100 * 20 / (120 * 10 + 5 * 40 + 100 * 20):.2f}% |")
+
+
 def test_w8a8_validation(lib):
     assert lib.flk_w8a8_gemm(FAKE, FAKE, FAKE, FAKE, 64, 192, 64, FAKE, 64, None, None) == _lib.FLK_E_UNSUPPORTED
     assert lib.flk_w8a8_gemm(FAKE, FAKE, FAKE, FAKE, 64, 256, 66, FAKE, 66, None, None) == _lib.FLK_E_UNSUPPORTED
